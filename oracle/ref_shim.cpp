@@ -1,0 +1,115 @@
+// extern "C" entry points over the reference's own CPU kernels, compiled from the reference sources where they lie
+// (oracle/Makefile passes their directory with -I). TEST INFRASTRUCTURE ONLY: the result, oracle/_ref/libidolref.so,
+// writes golden vectors (tests/golden/make_golden.py), validates the oracle restatement (tests/test_oracle.py) and
+// is the timed CPU baseline in bench.py. It is never part of the product.
+//
+// kernels.cpp and decoders.cpp are included as one translation unit so that the helpers they keep in anonymous
+// namespaces (quantize_activations, norm_rows, gelu_tanh) can be called directly; nothing in them is modified.
+#include "kernels.cpp"
+#include "decoders.cpp"
+
+#include <cstdint>
+#include <exception>
+#include <vector>
+
+namespace {
+
+thread_local int g_status = 0;
+
+template <typename F>
+int guarded(F&& f) {
+    try {
+        f();
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+// 1 when the integer (AVX-VNNI) kernel can run on this CPU.
+int ref_quant_int8_supported() { return idol::detail::quant_int8_supported() ? 1 : 0; }
+
+// quantized_linear + gemm_packed. mode: 0 float kernel, 1 integer kernel (as set_quant_kernel).
+int ref_gemm_panel(const float* a, int m, const std::uint8_t* blob, std::int64_t blob_bytes, const float* bias,
+                   int out, int in, int bits, int group, int n_offset, int n, const float* residual, int gelu,
+                   float* c, int mode) {
+    return guarded([&] {
+        std::vector<std::uint8_t> b(blob, blob + blob_bytes);
+        std::vector<float> bv(bias, bias + out);
+        const auto w = idol::detail::quantized_linear(std::move(b), bv, out, in, bits, group);
+        idol::detail::set_quant_kernel(mode);
+        idol::detail::gemm_packed(a, m, w, n_offset, n, residual, gelu != 0, c);
+        idol::detail::set_quant_kernel(-1);
+    });
+}
+
+// pack_linear + gemm_packed on dense fp32 weights [out x in].
+int ref_gemm_dense(const float* a, int m, const float* weight, const float* bias, int out, int in, int n_offset,
+                   int n, const float* residual, int gelu, float* c) {
+    return guarded([&] {
+        std::vector<float> wv(weight, weight + (std::size_t)out * in), bv(bias, bias + out);
+        const auto w = idol::detail::pack_linear(wv, bv, out, in);
+        idol::detail::gemm_packed(a, m, w, n_offset, n, residual, gelu != 0, c);
+    });
+}
+
+// quantized_linear + dequantize_linear: the weights [out x in] the GEMM sees. Returns -1 when quantized_linear
+// rejects the shape or blob.
+int ref_dequantize_panel(const std::uint8_t* blob, std::int64_t blob_bytes, int out, int in, int bits, int group,
+                         float* weight) {
+    return guarded([&] {
+        std::vector<std::uint8_t> b(blob, blob + blob_bytes);
+        std::vector<float> bias(out, 0.0f);
+        const auto w = idol::detail::quantized_linear(std::move(b), bias, out, in, bits, group);
+        const auto d = idol::detail::dequantize_linear(w);
+        std::copy(d.begin(), d.end(), weight);
+    });
+}
+
+std::int64_t ref_quant_panel_bytes(int in, int bits, int group) {
+    return (std::int64_t)idol::detail::quant_panel_bytes(in, bits, group);
+}
+
+// The integer kernel's activation quantization for group 32 (rows [0, m), no padding rows).
+int ref_quantize_activations(const float* a, int m, int k, std::int8_t* qa, float* scale, std::int32_t* qsum) {
+#ifdef IDOL_VNNI_PATH
+    idol::detail::quantize_activations(a, m, m, k, 32, qa, scale, qsum);
+    return 0;
+#else
+    (void)a, (void)m, (void)k, (void)qa, (void)scale, (void)qsum;
+    return -1;
+#endif
+}
+
+void ref_layer_norm(const float* x, int rows, int dim, const float* gamma, const float* beta, float* y) {
+    idol::detail::layer_norm(x, rows, dim, gamma, beta, y);
+}
+
+void ref_norm_rows(const float* x, float* y, int rows, int dim, float eps, const float* gamma, const float* beta,
+                   const float* shift, const float* scale) {
+    idol::norm_rows(x, y, rows, dim, eps, gamma, beta, shift, scale);
+}
+
+void ref_attention(const float* q, int lq, int ldq, const float* k, const float* v, int lk, int ldkv, int heads,
+                   int head_dim, float* out, int dim) {
+    idol::detail::attention(q, lq, ldq, k, v, lk, ldkv, heads, head_dim, out, dim);
+}
+
+void ref_gelu_tanh(float* x, std::int64_t count) { idol::gelu_tanh(x, (std::size_t)count); }
+
+// exp256 / gelu256 over count values (count a multiple of 8) and gelu_scalar over count values.
+void ref_exp256(const float* x, std::int64_t count, float* y) {
+    for (std::int64_t i = 0; i + 8 <= count; i += 8) _mm256_storeu_ps(y + i, idol::detail::exp256(_mm256_loadu_ps(x + i)));
+}
+void ref_gelu256(const float* x, std::int64_t count, float* y) {
+    for (std::int64_t i = 0; i + 8 <= count; i += 8) _mm256_storeu_ps(y + i, idol::detail::gelu256(_mm256_loadu_ps(x + i)));
+}
+void ref_gelu_scalar(const float* x, std::int64_t count, float* y) {
+    for (std::int64_t i = 0; i < count; ++i) y[i] = idol::detail::gelu_scalar(x[i]);
+}
+
+}  // extern "C"
