@@ -1,0 +1,283 @@
+// Non-causal multi-head attention for gfx950.
+//
+// attn_mfma_hd64 (bf16/fp16 inputs, head_dim 64): a flash-style kernel. A workgroup of 4 waves owns 128 queries of
+// one (batch, head); each wave owns 32 queries. Key/value tiles of 64 rows are staged in LDS (K as [key][d],
+// V transposed to [d][key] in fp16) and shared by the 4 waves. Scores are computed transposed, S^T = K * Q^T, so a
+// lane holds 32 scores of a single query (its column) and the online softmax (fp32, base-2 exponent with the
+// 1/sqrt(64) * log2(e) factor folded in) needs one cross-lane exchange (lanes l and l + 32). The probabilities stay in
+// registers and become, converted to fp16, the B operand of O^T = V^T * P^T; the MFMA's k order is permuted to the
+// order in which the score accumulator holds the keys, and the V^T operand is read in that same order.
+//
+// attn_f32 (any dtype, head_dim <= 256): one wave per (query, head, batch), 64 keys per step with one key per lane
+// for the scores and the head dimension split over lanes for P * V; fp32 throughout. Used for fp32 activations
+// (the reference's float attention surface) and head sizes other than 64.
+#include "common.h"
+
+#include <type_traits>
+
+namespace idolq {
+namespace {
+
+struct AttnParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* out;
+    int dt, out_dt;
+    int64_t lq, lk, heads, head_dim;
+    int64_t ldq, ldkv, q_bs, kv_bs, ldo, o_bs;
+    float scale_log2;  // log2(e) / sqrt(head_dim)
+};
+
+constexpr int kHD = 64;
+constexpr int kBQ = 128;
+constexpr int kBKV = 64;
+constexpr int kKPitch = kHD + 8;    // elements per key row of K in LDS (144 bytes: conflict-free 16-byte reads)
+constexpr int kVPitch = kBKV + 4;   // elements per d row of V^T in LDS (136 bytes: conflict-free 8-byte reads)
+
+template <typename T>
+struct AttnMfma;
+template <>
+struct AttnMfma<__bf16> {
+    typedef bf16x8 vec;
+    static __device__ __forceinline__ f32x16 run(vec a, vec b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+};
+template <>
+struct AttnMfma<_Float16> {
+    typedef f16x8 vec;
+    static __device__ __forceinline__ f32x16 run(vec a, vec b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <typename T>
+__device__ __forceinline__ _Float16 to_half(uint16_t bits) {
+    if (std::is_same<T, _Float16>::value) return __builtin_bit_cast(_Float16, bits);
+    return static_cast<_Float16>(bf16_bits_to_float(bits));
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void attn_mfma_hd64(AttnParams p) {
+    typedef typename AttnMfma<T>::vec Vec;
+    __shared__ __attribute__((aligned(16))) uint16_t k_lds[kBKV * kKPitch];
+    __shared__ __attribute__((aligned(16))) uint16_t vt_lds[kHD * kVPitch];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t b = blockIdx.z, h = blockIdx.y;
+    const int64_t q0 = (int64_t)blockIdx.x * kBQ + wave * 32;
+    const int64_t qi = q0 + (lane & 31);
+    const int half = lane >> 5;
+
+    const uint16_t* qbase = static_cast<const uint16_t*>(p.q) + b * p.q_bs + h * kHD;
+    const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + b * p.kv_bs + h * kHD;
+    const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + b * p.kv_bs + h * kHD;
+
+    // Q^T operand: lane supplies query qi, d = 16 c + 8 half + e.
+    Vec qf[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        uint4 raw = make_uint4(0, 0, 0, 0);
+        if (qi < p.lq) raw = *reinterpret_cast<const uint4*>(qbase + qi * p.ldq + 16 * c + 8 * half);
+        qf[c] = __builtin_bit_cast(Vec, raw);
+    }
+
+    f32x16 o[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[t][r] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    for (int64_t j0 = 0; j0 < p.lk; j0 += kBKV) {
+        __syncthreads();
+        // Stage K [key][d] and V^T [d][key]: 512 sixteen-byte units each, 2 per thread.
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int u = threadIdx.x + i * 256;
+            const int key = u >> 3, part = u & 7;
+            uint4 kr = make_uint4(0, 0, 0, 0), vr = make_uint4(0, 0, 0, 0);
+            if (j0 + key < p.lk) {
+                kr = *reinterpret_cast<const uint4*>(kbase + (j0 + key) * p.ldkv + 8 * part);
+                vr = *reinterpret_cast<const uint4*>(vbase + (j0 + key) * p.ldkv + 8 * part);
+            }
+            *reinterpret_cast<uint4*>(k_lds + key * kKPitch + 8 * part) = kr;
+            const uint32_t vw[4] = {vr.x, vr.y, vr.z, vr.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint16_t bits = (uint16_t)(vw[e >> 1] >> (16 * (e & 1)));
+                vt_lds[(8 * part + e) * kVPitch + key] = __builtin_bit_cast(uint16_t, to_half<T>(bits));
+            }
+        }
+        __syncthreads();
+
+        // S^T for 64 keys: two 32-key sub-tiles, 4 MFMAs each over d.
+        f32x16 s[2];
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[st][r] = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const Vec a = *reinterpret_cast<const Vec*>(k_lds + (st * 32 + (lane & 31)) * kKPitch + 16 * c + 8 * half);
+                s[st] = AttnMfma<T>::run(a, qf[c], s[st]);
+            }
+        }
+        // Online softmax for query qi over the 64 keys (32 here, 32 in lane ^ 32).
+        float mx = -INFINITY;
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t key = j0 + st * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                const float t = key < p.lk ? s[st][r] * p.scale_log2 : -INFINITY;
+                s[st][r] = t;
+                mx = fmaxf(mx, t);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = exp2f(m_run - m_new);
+        float lsum = 0.0f;
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float e = exp2f(s[st][r] - m_new);
+                s[st][r] = e;
+                lsum += e;
+            }
+        lsum += __shfl_xor(lsum, 32);
+        l_run = l_run * alpha + lsum;
+        m_run = m_new;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+
+        // O^T += V^T * P^T over 4 chunks of 16 keys. Chunk (st, kc) uses accumulator elements r = 8 kc + e of
+        // sub-tile st; slot 8 * half + e of the MFMA's k holds key st*32 + 16 kc + 8 (e / 4) + 4 half + e % 4.
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+            for (int kc = 0; kc < 2; ++kc) {
+                f16x8 pf;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) pf[e] = static_cast<_Float16>(s[st][8 * kc + e]);
+                const int key0 = st * 32 + 16 * kc + 4 * half;
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const int d = t * 32 + (lane & 31);
+                    const uint2 lo = *reinterpret_cast<const uint2*>(vt_lds + d * kVPitch + key0);
+                    const uint2 hi = *reinterpret_cast<const uint2*>(vt_lds + d * kVPitch + key0 + 8);
+                    const f16x8 va = __builtin_bit_cast(f16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pf, o[t], 0, 0, 0);
+                }
+            }
+    }
+
+    if (qi >= p.lq) return;
+    const float inv = 1.0f / l_run;
+    const int64_t obase = b * p.o_bs + qi * p.ldo + h * kHD;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int d = t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+            store_from_float(p.out, p.out_dt, obase + d, o[t][r] * inv);
+        }
+}
+
+// ------------------------------------------------------------------------------------------------ fp32 kernel
+constexpr int kMaxHD = 256;
+
+__global__ __launch_bounds__(64) void attn_f32(AttnParams p) {
+    __shared__ float qs[kMaxHD];
+    __shared__ float ps[64];
+    const int lane = threadIdx.x;
+    const int64_t qi = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int64_t hd = p.head_dim;
+    const int64_t qo = b * p.q_bs + qi * p.ldq + h * hd;
+    for (int64_t d = lane; d < hd; d += 64) qs[d] = load_as_float(p.q, p.dt, qo + d);
+    __syncthreads();
+    const float scale = 1.0f / sqrtf((float)hd);
+    float acc[kMaxHD / 64];
+#pragma unroll
+    for (int i = 0; i < kMaxHD / 64; ++i) acc[i] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+    const int64_t kvo = b * p.kv_bs + h * hd;
+    for (int64_t j0 = 0; j0 < p.lk; j0 += 64) {
+        const int64_t j = j0 + lane;
+        float sc = -INFINITY;
+        if (j < p.lk) {
+            float dot = 0.0f;
+            for (int64_t d = 0; d < hd; ++d) dot = fmaf(qs[d], load_as_float(p.k, p.dt, kvo + j * p.ldkv + d), dot);
+            sc = dot * scale;
+        }
+        float mx = sc;
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = expf(m_run - m_new);
+        const float e = j < p.lk ? expf(sc - m_new) : 0.0f;
+        float sum = e;
+        for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+        l_run = l_run * alpha + sum;
+        m_run = m_new;
+        __syncthreads();
+        ps[lane] = e;
+        __syncthreads();
+        const int64_t nk = p.lk - j0 < 64 ? p.lk - j0 : 64;
+#pragma unroll
+        for (int i = 0; i < kMaxHD / 64; ++i) {
+            const int64_t d = lane + 64 * i;
+            if (d < hd) {
+                float a = acc[i] * alpha;
+                for (int64_t t = 0; t < nk; ++t) a = fmaf(ps[t], load_as_float(p.v, p.dt, kvo + (j0 + t) * p.ldkv + d), a);
+                acc[i] = a;
+            }
+        }
+    }
+    const float inv = 1.0f / l_run;
+    const int64_t oo = b * p.o_bs + qi * p.ldo + h * hd;
+#pragma unroll
+    for (int i = 0; i < kMaxHD / 64; ++i) {
+        const int64_t d = lane + 64 * i;
+        if (d < hd) store_from_float(p.out, p.out_dt, oo + d, acc[i] * inv);
+    }
+}
+
+}  // namespace
+}  // namespace idolq
+
+using namespace idolq;
+
+extern "C" int idolq_attention(const void* q, const void* k, const void* v, int dtype, int64_t batch, int64_t lq,
+                               int64_t lk, int64_t heads, int64_t head_dim, int64_t ldq, int64_t ldkv, int64_t q_bs,
+                               int64_t kv_bs, void* out, int out_dtype, int64_t ldo, int64_t o_bs, void* stream) {
+    if (!q || !k || !v || !out) return fail(IDOLQ_EINVAL, "q, k, v and out must be non-null");
+    if (!dtype_ok(dtype) || !dtype_ok(out_dtype)) return fail(IDOLQ_EINVAL, "unknown dtype code");
+    if (batch < 0 || lq < 0 || lk <= 0 || heads <= 0 || head_dim <= 0 || head_dim > kMaxHD)
+        return fail(IDOLQ_EINVAL, "bad attention shape (needs lk > 0 and 0 < head_dim <= 256)");
+    const int64_t dim = heads * head_dim;
+    if (ldq < dim || ldkv < dim || ldo < dim) return fail(IDOLQ_EINVAL, "row stride smaller than heads * head_dim");
+    if (batch > 65535 || heads > 65535 || lq > 0x7fffffff) return fail(IDOLQ_EINVAL, "grid too large");
+    if (batch == 0 || lq == 0) return IDOLQ_OK;
+    AttnParams p{q, k, v, out, dtype, out_dtype, lq, lk, heads, head_dim, ldq, ldkv, q_bs, kv_bs, ldo, o_bs,
+                 1.4426950408889634f / sqrtf((float)head_dim)};
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const size_t esz = dtype_size(dtype);
+    const bool aligned = reinterpret_cast<uintptr_t>(q) % 16 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(v) % 16 == 0 && (ldq * esz) % 16 == 0 &&
+                         (ldkv * esz) % 16 == 0 && (q_bs * esz) % 16 == 0 && (kv_bs * esz) % 16 == 0;
+    if (dtype != IDOLQ_F32 && head_dim == kHD && aligned) {
+        const dim3 grid((unsigned)((lq + kBQ - 1) / kBQ), (unsigned)heads, (unsigned)batch);
+        if (dtype == IDOLQ_BF16)
+            hipLaunchKernelGGL(attn_mfma_hd64<__bf16>, grid, dim3(256), 0, s, p);
+        else
+            hipLaunchKernelGGL(attn_mfma_hd64<_Float16>, grid, dim3(256), 0, s, p);
+        return check_launch("attn_mfma_hd64");
+    }
+    const dim3 grid((unsigned)lq, (unsigned)heads, (unsigned)batch);
+    hipLaunchKernelGGL(attn_f32, grid, dim3(64), 0, s, p);
+    return check_launch("attn_f32");
+}

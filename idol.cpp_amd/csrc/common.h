@@ -1,0 +1,81 @@
+// Shared definitions for the gfx950 kernels of libidolq: vector types for the MFMA builtins, dtype conversion,
+// error reporting for the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "../../include/idolq.h"
+
+namespace idolq {
+
+// Operand and accumulator vectors of the gfx950 MFMA builtins.
+typedef __bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(__bf16))));
+typedef _Float16 f16x8 __attribute__((__vector_size__(8 * sizeof(_Float16))));
+typedef int i32x4 __attribute__((__vector_size__(4 * sizeof(int))));
+typedef float f32x4 __attribute__((__vector_size__(4 * sizeof(float))));
+typedef float f32x16 __attribute__((__vector_size__(16 * sizeof(float))));
+typedef int i32x16 __attribute__((__vector_size__(16 * sizeof(int))));
+
+constexpr int kQ8Block = 32;  // k values per Q8_0 block
+constexpr int kQ8Bytes = 34;  // fp16 scale + 32 int8 codes
+
+// ------------------------------------------------------------------------------------------------ host: errors
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int check_launch(const char* what);
+inline bool dtype_ok(int dt) { return dt == IDOLQ_F32 || dt == IDOLQ_F16 || dt == IDOLQ_BF16; }
+inline size_t dtype_size(int dt) { return dt == IDOLQ_F32 ? 4 : 2; }
+
+// ------------------------------------------------------------------------------------------------ device: dtypes
+__device__ __forceinline__ float half_bits_to_float(uint16_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+__device__ __forceinline__ float bf16_bits_to_float(uint16_t b) {
+    return __builtin_bit_cast(float, static_cast<uint32_t>(b) << 16);
+}
+
+// Round-to-nearest-even conversions (the hardware's default conversion mode).
+__device__ __forceinline__ uint16_t float_to_bf16_bits(float f) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f)); }
+__device__ __forceinline__ uint16_t float_to_half_bits(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
+
+// Load element i of a buffer of the given dtype as fp32.
+__device__ __forceinline__ float load_as_float(const void* p, int dt, int64_t i) {
+    if (dt == IDOLQ_F32) return static_cast<const float*>(p)[i];
+    const uint16_t b = static_cast<const uint16_t*>(p)[i];
+    return dt == IDOLQ_BF16 ? bf16_bits_to_float(b) : half_bits_to_float(b);
+}
+
+__device__ __forceinline__ void store_from_float(void* p, int dt, int64_t i, float v) {
+    if (dt == IDOLQ_F32) {
+        static_cast<float*>(p)[i] = v;
+    } else {
+        static_cast<uint16_t*>(p)[i] = dt == IDOLQ_BF16 ? float_to_bf16_bits(v) : float_to_half_bits(v);
+    }
+}
+
+// Round a float through a dtype and back (identity for fp32).
+__device__ __forceinline__ float round_through(int dt, float v) {
+    if (dt == IDOLQ_BF16) return bf16_bits_to_float(float_to_bf16_bits(v));
+    if (dt == IDOLQ_F16) return half_bits_to_float(float_to_half_bits(v));
+    return v;
+}
+
+// ------------------------------------------------------------------------------------------------ activations
+__device__ __forceinline__ float apply_act(int act, float v) {
+    switch (act) {
+        case IDOLQ_ACT_GELU_ERF: return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+        case IDOLQ_ACT_GELU_TANH: {
+            const float u = 0.7978845608028654f * (v + 0.044715f * v * v * v);
+            return 0.5f * v * (1.0f + tanhf(u));
+        }
+        case IDOLQ_ACT_RELU: return v > 0.0f ? v : 0.0f;
+        default: return v;
+    }
+}
+
+}  // namespace idolq

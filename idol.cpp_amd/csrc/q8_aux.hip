@@ -1,0 +1,245 @@
+// Entry points around the Q8_0 GEMM: the C ABI's error slot and version, Q8_0 expansion, the int8 activation
+// quantizer, activations, the sine/cosine position embedding and a strided copy.
+#include "common.h"
+
+#include <cstdio>
+
+namespace idolq {
+
+namespace {
+thread_local std::string g_error;
+}
+
+void set_error(const std::string& msg) { g_error = msg; }
+
+int fail(int code, const std::string& msg) {
+    g_error = msg;
+    return code;
+}
+
+int check_launch(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(IDOLQ_ELAUNCH, std::string(what) + ": " + hipGetErrorString(e));
+    return IDOLQ_OK;
+}
+
+namespace {
+
+// ------------------------------------------------------------------------------------------------ Q8_0 expansion
+// One thread per Q8_0 block: 32 outputs fp32(d) * q rounded to the output dtype, written as 16-byte stores.
+__global__ __launch_bounds__(256) void q8_dequant_kernel(const uint8_t* __restrict__ w, int64_t blocks, void* out,
+                                                         int out_dt) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= blocks) return;
+    const uint8_t* blk = w + b * kQ8Bytes;
+    const float d = half_bits_to_float((uint16_t)(blk[0] | (blk[1] << 8)));
+    if (out_dt == IDOLQ_F32) {
+        float* o = static_cast<float*>(out) + b * kQ8Block;
+        for (int t = 0; t < kQ8Block; t += 4) {
+            float4 v;
+            v.x = (float)(int8_t)blk[2 + t] * d;
+            v.y = (float)(int8_t)blk[3 + t] * d;
+            v.z = (float)(int8_t)blk[4 + t] * d;
+            v.w = (float)(int8_t)blk[5 + t] * d;
+            *reinterpret_cast<float4*>(o + t) = v;
+        }
+    } else {
+        uint16_t* o = static_cast<uint16_t*>(out) + b * kQ8Block;
+        for (int t = 0; t < kQ8Block; t += 8) {
+            uint32_t packed[4];
+            for (int e = 0; e < 4; ++e) {
+                const float lo = (float)(int8_t)blk[2 + t + 2 * e] * d, hi = (float)(int8_t)blk[3 + t + 2 * e] * d;
+                const uint16_t l = out_dt == IDOLQ_BF16 ? float_to_bf16_bits(lo) : float_to_half_bits(lo);
+                const uint16_t h = out_dt == IDOLQ_BF16 ? float_to_bf16_bits(hi) : float_to_half_bits(hi);
+                packed[e] = (uint32_t)l | ((uint32_t)h << 16);
+            }
+            *reinterpret_cast<uint4*>(o + t) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ Q8_0 quantizer
+// One thread per 32-value block of an fp32 [n x k] matrix: d = amax / 127, id = d ? 1 / d : 0,
+// q = round-half-away-from-zero(x * id), d stored as fp16 (ggml's quantize_row_q8_0_ref, the rule gguf-py's
+// Q8_0.quantize_blocks restates). The quotient and the product are IEEE fp32, so the codes match a CPU run of the
+// same rule bit for bit.
+__global__ __launch_bounds__(256) void q8_quantize_kernel(const float* __restrict__ w, int64_t nb, int64_t blocks,
+                                                          int64_t ldw, uint8_t* __restrict__ out) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= blocks) return;
+    const int64_t r = b / nb, g = b - r * nb;
+    const float* x = w + r * ldw + g * kQ8Block;
+    float v[kQ8Block];
+    float amax = 0.0f;
+    for (int t = 0; t < kQ8Block; ++t) {
+        v[t] = x[t];
+        amax = fmaxf(amax, fabsf(v[t]));
+    }
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint8_t* o = out + b * kQ8Bytes;
+    const uint16_t dh = float_to_half_bits(d);
+    o[0] = (uint8_t)(dh & 0xff);
+    o[1] = (uint8_t)(dh >> 8);
+    for (int t = 0; t < kQ8Block; ++t) o[2 + t] = (uint8_t)(int8_t)roundf(v[t] * id);
+}
+
+// ------------------------------------------------------------------------------------------------ int8 activations
+// One thread per (row, 32-block): amax, s = amax / 127, inv = 127 / amax, q = rint(x * inv). Division and the
+// product are IEEE fp32 (correctly rounded), rint rounds ties to even: the same operations, in the same order, as
+// the reference's quantize_activations, so qa, s and qsum are bit-identical.
+__global__ __launch_bounds__(256) void quantize_act_kernel(const void* __restrict__ x, int x_dt, int64_t m,
+                                                           int64_t nb, int64_t ldx, int8_t* __restrict__ qa,
+                                                           float* __restrict__ scale, int32_t* __restrict__ qsum) {
+    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= m * nb) return;
+    const int64_t r = id / nb, g = id - r * nb;
+    float v[kQ8Block];
+    const int64_t base = r * ldx + g * kQ8Block;
+    for (int t = 0; t < kQ8Block; ++t) v[t] = load_as_float(x, x_dt, base + t);
+    float amax = 0.0f;
+    for (int t = 0; t < kQ8Block; ++t) amax = fmaxf(amax, fabsf(v[t]));
+    const float s = amax / 127.0f;
+    const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+    int32_t sum = 0;
+    uint32_t words[8];
+    for (int t = 0; t < kQ8Block; t += 4) {
+        uint32_t word = 0;
+        for (int e = 0; e < 4; ++e) {
+            const int32_t q = (int32_t)rintf(v[t + e] * inv);
+            sum += q;
+            word |= (uint32_t)(uint8_t)(int8_t)q << (8 * e);
+        }
+        words[t / 4] = word;
+    }
+    int8_t* dst = qa + r * (nb * kQ8Block) + g * kQ8Block;
+    *reinterpret_cast<uint4*>(dst) = make_uint4(words[0], words[1], words[2], words[3]);
+    *reinterpret_cast<uint4*>(dst + 16) = make_uint4(words[4], words[5], words[6], words[7]);
+    scale[id] = s;
+    if (qsum) qsum[id] = sum;
+}
+
+// ------------------------------------------------------------------------------------------------ elementwise
+__global__ __launch_bounds__(256) void activation_kernel(void* x, int dt, int64_t count, int act) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride)
+        store_from_float(x, dt, i, apply_act(act, load_as_float(x, dt, i)));
+}
+
+__global__ __launch_bounds__(256) void pos_embed_kernel(const float* __restrict__ coords, int64_t rows,
+                                                        const float* __restrict__ freqs, int nfreq, void* out,
+                                                        int out_dt, int64_t ldo) {
+    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t per_row = 3 * (int64_t)nfreq;
+    if (id >= rows * per_row) return;
+    const int64_t r = id / per_row;
+    const int rem = (int)(id - r * per_row);
+    const int c = rem / nfreq, j = rem - c * nfreq;
+    const float kPi = 3.14159265358979323846f;
+    const float ang = (coords[r * 3 + c] * freqs[j]) * kPi;
+    const int64_t o = r * ldo + (int64_t)c * 2 * nfreq + j;
+    store_from_float(out, out_dt, o, sinf(ang));
+    store_from_float(out, out_dt, o + nfreq, cosf(ang));
+}
+
+__global__ __launch_bounds__(256) void copy2d_kernel(const void* src, int sdt, int64_t lds, void* dst, int ddt,
+                                                     int64_t ldd, int64_t rows, int64_t cols) {
+    const int64_t total = rows * cols, stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+        const int64_t r = i / cols, c = i - r * cols;
+        store_from_float(dst, ddt, r * ldd + c, load_as_float(src, sdt, r * lds + c));
+    }
+}
+
+unsigned grid_for(int64_t items, int threads = 256) {
+    const int64_t g = (items + threads - 1) / threads;
+    return (unsigned)(g < 1 ? 1 : g > 1048576 ? 1048576 : g);
+}
+
+}  // namespace
+
+int quantize_act_launch(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, int8_t* qa, float* scale,
+                        int32_t* qsum, hipStream_t stream) {
+    const int64_t nb = k / kQ8Block;
+    if (m * nb == 0) return IDOLQ_OK;
+    hipLaunchKernelGGL(quantize_act_kernel, dim3((unsigned)((m * nb + 255) / 256)), dim3(256), 0, stream, x, x_dtype, m,
+                       nb, ldx, qa, scale, qsum);
+    return check_launch("quantize_act_kernel");
+}
+
+}  // namespace idolq
+
+using namespace idolq;
+
+extern "C" const char* idolq_last_error(void) { return g_error.c_str(); }
+
+extern "C" const char* idolq_version(void) { return "libidolq 0.1 gfx950"; }
+
+extern "C" int64_t idolq_q8_0_bytes(int64_t n, int64_t k) {
+    if (n < 0 || k < 0 || k % kQ8Block) return 0;
+    return n * (k / kQ8Block) * kQ8Bytes;
+}
+
+extern "C" int idolq_q8_0_dequant(const uint8_t* w, int64_t n, int64_t k, void* out, int out_dtype, void* stream) {
+    if (!w || !out) return fail(IDOLQ_EINVAL, "w and out must be non-null");
+    if (!dtype_ok(out_dtype)) return fail(IDOLQ_EINVAL, "unknown dtype code");
+    if (n < 0 || k <= 0 || k % kQ8Block) return fail(IDOLQ_EINVAL, "need n >= 0 and k a positive multiple of 32");
+    if (reinterpret_cast<uintptr_t>(out) % 16 != 0) return fail(IDOLQ_EINVAL, "out must be 16-byte aligned");
+    const int64_t blocks = n * (k / kQ8Block);
+    if (blocks == 0) return IDOLQ_OK;
+    hipLaunchKernelGGL(q8_dequant_kernel, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), w, blocks, out, out_dtype);
+    return check_launch("q8_dequant_kernel");
+}
+
+extern "C" int idolq_q8_0_quantize(const float* w, int64_t n, int64_t k, int64_t ldw, uint8_t* out, void* stream) {
+    if (!w || !out) return fail(IDOLQ_EINVAL, "w and out must be non-null");
+    if (n < 0 || k <= 0 || k % kQ8Block || ldw < k) return fail(IDOLQ_EINVAL, "need n >= 0, k a positive multiple of 32, ldw >= k");
+    const int64_t nb = k / kQ8Block, blocks = n * nb;
+    if (blocks == 0) return IDOLQ_OK;
+    hipLaunchKernelGGL(q8_quantize_kernel, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), w, nb, blocks, ldw, out);
+    return check_launch("q8_quantize_kernel");
+}
+
+extern "C" int idolq_quantize_act_q8(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, int8_t* qa,
+                                     float* scale, int32_t* qsum, void* stream) {
+    if (!x || !qa || !scale) return fail(IDOLQ_EINVAL, "x, qa and scale must be non-null");
+    if (!dtype_ok(x_dtype)) return fail(IDOLQ_EINVAL, "unknown dtype code");
+    if (m < 0 || k <= 0 || k % kQ8Block || ldx < k) return fail(IDOLQ_EINVAL, "need m >= 0, k a positive multiple of 32, ldx >= k");
+    if (reinterpret_cast<uintptr_t>(qa) % 16 != 0) return fail(IDOLQ_EINVAL, "qa must be 16-byte aligned");
+    return quantize_act_launch(x, x_dtype, m, k, ldx, qa, scale, qsum, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int idolq_activation(void* x, int dtype, int64_t count, int act, void* stream) {
+    if (!x && count > 0) return fail(IDOLQ_EINVAL, "x must be non-null");
+    if (!dtype_ok(dtype)) return fail(IDOLQ_EINVAL, "unknown dtype code");
+    if (act < IDOLQ_ACT_NONE || act > IDOLQ_ACT_RELU) return fail(IDOLQ_EINVAL, "unknown activation");
+    if (count <= 0 || act == IDOLQ_ACT_NONE) return IDOLQ_OK;
+    hipLaunchKernelGGL(activation_kernel, dim3(grid_for(count)), dim3(256), 0, static_cast<hipStream_t>(stream), x,
+                       dtype, count, act);
+    return check_launch("activation_kernel");
+}
+
+extern "C" int idolq_pos_embed(const float* coords, int64_t rows, const float* freqs, int64_t nfreq, void* out,
+                               int out_dtype, int64_t ldo, void* stream) {
+    if (!coords || !freqs || !out) return fail(IDOLQ_EINVAL, "coords, freqs and out must be non-null");
+    if (!dtype_ok(out_dtype)) return fail(IDOLQ_EINVAL, "unknown dtype code");
+    if (rows < 0 || nfreq <= 0 || nfreq > 65536 || ldo < 6 * nfreq) return fail(IDOLQ_EINVAL, "bad pos_embed shape");
+    if (rows == 0) return IDOLQ_OK;
+    const int64_t items = rows * 3 * nfreq;
+    hipLaunchKernelGGL(pos_embed_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), coords, rows, freqs, (int)nfreq, out, out_dtype, ldo);
+    return check_launch("pos_embed_kernel");
+}
+
+extern "C" int idolq_copy2d(const void* src, int src_dtype, int64_t lds, void* dst, int dst_dtype, int64_t ldd,
+                            int64_t rows, int64_t cols, void* stream) {
+    if (!src || !dst) return fail(IDOLQ_EINVAL, "src and dst must be non-null");
+    if (!dtype_ok(src_dtype) || !dtype_ok(dst_dtype)) return fail(IDOLQ_EINVAL, "unknown dtype code");
+    if (rows < 0 || cols < 0 || lds < cols || ldd < cols) return fail(IDOLQ_EINVAL, "bad copy shape");
+    if (rows * cols == 0) return IDOLQ_OK;
+    hipLaunchKernelGGL(copy2d_kernel, dim3(grid_for(rows * cols)), dim3(256), 0, static_cast<hipStream_t>(stream), src,
+                       src_dtype, lds, dst, dst_dtype, ldd, rows, cols);
+    return check_launch("copy2d_kernel");
+}

@@ -1,0 +1,251 @@
+"""ctypes binding of libidolq.so (include/idolq.h) over PyTorch-ROCm tensors.
+
+PyTorch supplies device memory and the current HIP stream; every computation runs in the library's HIP kernels.
+There is no fallback: if the library is missing or a call fails, a Python exception is raised.
+"""
+import ctypes
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libidolq.so"
+
+F32, F16, BF16 = 0, 1, 2
+ACT_NONE, ACT_GELU_ERF, ACT_GELU_TANH, ACT_RELU = 0, 1, 2, 3
+MODE_AUTO, MODE_DEQUANT, MODE_EXACT, MODE_INT8 = 0, 1, 2, 3
+FLAG_ROUND_BEFORE_BIAS = 1
+EINVAL, ELAUNCH, ENOSUPPORT = -1, -2, -3
+
+DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+Q8_0_BLOCK, Q8_0_BYTES = 32, 34
+
+_vp, _i64, _int, _sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_size_t
+
+# name: (restype, argtypes)
+_SIGNATURES = {
+    "idolq_last_error": (ctypes.c_char_p, []),
+    "idolq_version": (ctypes.c_char_p, []),
+    "idolq_q8_0_bytes": (_i64, [_i64, _i64]),
+    "idolq_q8_0_gemm": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _int, _vp, _int, _i64, _int,
+                               _int, _int, _vp, _int, _i64, _vp, _sz, _vp]),
+    "idolq_q8_0_gemm_workspace": (_sz, [_i64, _i64, _int]),
+    "idolq_q8_0_quantize": (_int, [_vp, _i64, _i64, _i64, _vp, _vp]),
+    "idolq_q8_0_dequant": (_int, [_vp, _i64, _i64, _vp, _int, _vp]),
+    "idolq_quantize_act_q8": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
+    "idolq_q8_0_block_dots": (_int, [_vp, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _vp]),
+    "idolq_layernorm": (_int, [_vp, _int, _i64, _i64, _i64, ctypes.c_float, _vp, _vp, _vp, _vp, _i64, _vp, _int, _i64,
+                               _vp]),
+    "idolq_attention": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _int,
+                               _i64, _i64, _vp]),
+    "idolq_activation": (_int, [_vp, _int, _i64, _int, _vp]),
+    "idolq_pos_embed": (_int, [_vp, _i64, _vp, _i64, _vp, _int, _i64, _vp]),
+    "idolq_copy2d": (_int, [_vp, _int, _i64, _vp, _int, _i64, _i64, _i64, _vp]),
+}
+
+_lib = None
+
+
+class IdolqError(RuntimeError):
+    """A failed library call that is not an argument error (launch failure, unsupported combination)."""
+
+
+def load():
+    """Load libidolq.so (built in-tree by `make -C idol.cpp_amd`); raises if it is absent."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"libidolq is not built: {LIB_PATH} is missing (run `make -C idol.cpp_amd`)")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def exported_symbols():
+    return list(_SIGNATURES)
+
+
+def _check(rc):
+    if rc != 0:
+        msg = load().idolq_last_error().decode()
+        if rc == EINVAL:
+            raise ValueError(msg)
+        raise IdolqError(msg)
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _code(t):
+    try:
+        return DTYPE_CODE[t.dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {t.dtype}") from None
+
+
+def _row_stride(t):
+    """Row stride (elements) of a 2-D tensor whose last dimension is unit-stride."""
+    if t.dim() != 2 or (t.shape[1] > 1 and t.stride(1) != 1):
+        raise ValueError("expected a 2-D tensor with a unit-stride last dimension")
+    return max(t.stride(0), t.shape[1]) if t.shape[0] > 1 else t.shape[1]
+
+
+def _require_cuda(*tensors):
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError("libidolq works on GPU tensors")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError("all tensors must be on the same device")
+    return dev
+
+
+def q8_0_bytes(n, k):
+    return int(load().idolq_q8_0_bytes(n, k))
+
+
+def gemm(x, w, n_total, n_offset=0, n=None, bias=None, residual=None, act=ACT_NONE, mode=MODE_AUTO, flags=0,
+         out=None, out_dtype=None, workspace=None):
+    """y = epilogue(x @ W[n_offset:n_offset+n]^T) with W raw Q8_0 blocks. x is [m, k] (unit-stride rows)."""
+    lib = load()
+    m, k = x.shape
+    if n is None:
+        n = n_total - n_offset
+    dev = _require_cuda(x, w, bias, residual, out, workspace)
+    if w.dtype != torch.uint8:
+        raise ValueError("Q8_0 weights are a uint8 tensor")
+    if w.numel() != q8_0_bytes(n_total, k) or not w.is_contiguous():
+        raise ValueError("Q8_0 weight size does not match its shape")
+    if out is None:
+        out = torch.empty((m, n), device=x.device, dtype=out_dtype or x.dtype)
+    if bias is not None and (bias.dim() != 1 or bias.numel() != n_total or not bias.is_contiguous()):
+        raise ValueError("bias must be a contiguous vector of n_total values")
+    ws_bytes = int(lib.idolq_q8_0_gemm_workspace(m, k, mode))
+    if ws_bytes and (workspace is None or workspace.numel() * workspace.element_size() < ws_bytes):
+        workspace = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8)
+    ldr = _row_stride(residual) if residual is not None else 0
+    _check(lib.idolq_q8_0_gemm(_ptr(x), _code(x), m, k, _row_stride(x), _ptr(w), n_total, n_offset, n, _ptr(bias),
+                               _code(bias) if bias is not None else 0, _ptr(residual),
+                               _code(residual) if residual is not None else 0, ldr, act, mode, flags, _ptr(out),
+                               _code(out), _row_stride(out), _ptr(workspace) if ws_bytes else None, ws_bytes,
+                               _stream(dev)))
+    return out
+
+
+def quantize_q8_0(w):
+    """Q8_0 blocks (uint8, n * k / 32 * 34 bytes) of an fp32 [n, k] GPU matrix."""
+    lib = load()
+    _require_cuda(w)
+    if w.dtype != torch.float32 or w.dim() != 2:
+        raise ValueError("quantize_q8_0 takes an fp32 matrix")
+    n, k = w.shape
+    out = torch.empty(q8_0_bytes(n, k), device=w.device, dtype=torch.uint8)
+    _check(lib.idolq_q8_0_quantize(_ptr(w), n, k, _row_stride(w), _ptr(out), _stream(w.device)))
+    return out
+
+
+def dequant(w, n, k, dtype):
+    lib = load()
+    _require_cuda(w)
+    out = torch.empty((n, k), device=w.device, dtype=dtype)
+    if w.numel() != q8_0_bytes(n, k):
+        raise ValueError("Q8_0 weight size does not match its shape")
+    _check(lib.idolq_q8_0_dequant(_ptr(w), n, k, _ptr(out), _code(out), _stream(w.device)))
+    return out
+
+
+def quantize_act(x, with_qsum=True):
+    """(qa int8 [m, k], scale fp32 [m, k/32], qsum int32 [m, k/32] or None) of the integer kernel."""
+    lib = load()
+    _require_cuda(x)
+    m, k = x.shape
+    qa = torch.empty((m, k), device=x.device, dtype=torch.int8)
+    sa = torch.empty((m, k // Q8_0_BLOCK), device=x.device, dtype=torch.float32)
+    qs = torch.empty((m, k // Q8_0_BLOCK), device=x.device, dtype=torch.int32) if with_qsum else None
+    _check(lib.idolq_quantize_act_q8(_ptr(x), _code(x), m, k, _row_stride(x), _ptr(qa), _ptr(sa), _ptr(qs),
+                                     _stream(x.device)))
+    return qa, sa, qs
+
+
+def block_dots(qa, w, n_total, n_offset=0, n=None):
+    lib = load()
+    _require_cuda(qa, w)
+    m, k = qa.shape
+    if n is None:
+        n = n_total - n_offset
+    if w.numel() != q8_0_bytes(n_total, k):
+        raise ValueError("Q8_0 weight size does not match its shape")
+    dots = torch.empty((m, n, k // Q8_0_BLOCK), device=qa.device, dtype=torch.int32)
+    _check(lib.idolq_q8_0_block_dots(_ptr(qa), m, k, _ptr(w), n_total, n_offset, n, _ptr(dots), _stream(qa.device)))
+    return dots
+
+
+def layernorm(x, eps, gamma=None, beta=None, shift=None, scale=None, rows_per_batch=0, out=None, out_dtype=None):
+    lib = load()
+    _require_cuda(x, gamma, beta, shift, scale, out)
+    rows, dim = x.shape
+    for v in (gamma, beta, shift, scale):
+        if v is not None and (v.dtype != torch.float32 or not v.is_contiguous()):
+            raise ValueError("gamma, beta, shift and scale are contiguous fp32 tensors")
+    if out is None:
+        out = torch.empty((rows, dim), device=x.device, dtype=out_dtype or x.dtype)
+    _check(lib.idolq_layernorm(_ptr(x), _code(x), rows, dim, _row_stride(x), eps, _ptr(gamma), _ptr(beta),
+                               _ptr(shift), _ptr(scale), rows_per_batch, _ptr(out), _code(out), _row_stride(out),
+                               _stream(x.device)))
+    return out
+
+
+def attention(q, k, v, batch, lq, lk, heads, head_dim, ldq, ldkv, q_bs, kv_bs, out, ldo, o_bs):
+    """Multi-head attention over flat buffers; q/k/v/out may be views into wider projection buffers."""
+    lib = load()
+    dev = _require_cuda(q, k, v, out)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError("q, k and v must share a dtype")
+    _check(lib.idolq_attention(_ptr(q), _ptr(k), _ptr(v), _code(q), batch, lq, lk, heads, head_dim, ldq, ldkv, q_bs,
+                               kv_bs, _ptr(out), _code(out), ldo, o_bs, _stream(dev)))
+    return out
+
+
+def activation(x, act):
+    lib = load()
+    _require_cuda(x)
+    if not x.is_contiguous():
+        raise ValueError("activation works in place on a contiguous tensor")
+    _check(lib.idolq_activation(_ptr(x), _code(x), x.numel(), act, _stream(x.device)))
+    return x
+
+
+def pos_embed(coords, freqs, out, ldo=None):
+    lib = load()
+    _require_cuda(coords, freqs, out)
+    rows = coords.shape[0]
+    if coords.dtype != torch.float32 or freqs.dtype != torch.float32:
+        raise ValueError("coords and freqs are fp32")
+    if ldo is None:
+        ldo = _row_stride(out)
+    _check(lib.idolq_pos_embed(_ptr(coords), rows, _ptr(freqs), freqs.numel(), _ptr(out), _code(out), ldo,
+                               _stream(coords.device)))
+    return out
+
+
+def copy2d(src, dst):
+    lib = load()
+    _require_cuda(src, dst)
+    rows, cols = src.shape
+    if dst.shape != src.shape:
+        raise ValueError("copy2d needs equal shapes")
+    _check(lib.idolq_copy2d(_ptr(src), _code(src), _row_stride(src), _ptr(dst), _code(dst), _row_stride(dst), rows,
+                            cols, _stream(src.device)))
+    return dst

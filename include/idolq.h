@@ -1,0 +1,137 @@
+/*
+ * libidolq: MI355X (gfx950) kernels for the Q8_0 block-quantized linear path of idol.cpp, behind a plain C ABI.
+ *
+ * Conventions
+ *   - Every pointer is device memory on the current HIP device, except where a comment says otherwise.
+ *   - `stream` is a hipStream_t passed as void* (NULL is the default stream). All calls are asynchronous on it and
+ *     allocate nothing; scratch that a call needs is passed in by the caller (workspace arguments).
+ *   - Return 0 on success or a negative IDOLQ_E* code; idolq_last_error() then describes the failure (the message
+ *     slot is thread-local). Argument errors are detected on the host before anything is launched.
+ *   - dtype codes: IDOLQ_F32, IDOLQ_F16, IDOLQ_BF16. Strides (ld*) are in elements.
+ *   - Q8_0 weights are the raw GGUF blocks: for each output row n, k / 32 blocks of 34 bytes, each a little-endian
+ *     fp16 scale d followed by 32 int8 codes q; the weight is w = fp32(d) * q.
+ */
+#ifndef IDOLQ_H
+#define IDOLQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { IDOLQ_F32 = 0, IDOLQ_F16 = 1, IDOLQ_BF16 = 2 };
+
+enum { IDOLQ_ACT_NONE = 0, IDOLQ_ACT_GELU_ERF = 1, IDOLQ_ACT_GELU_TANH = 2, IDOLQ_ACT_RELU = 3 };
+
+/* GEMM arithmetic.
+ *   DEQUANT  weights dequantized to the activation's 16-bit type (bf16 or fp16 of fp32(d) * q) in LDS, MFMA with fp32
+ *            accumulation over the whole depth: the numerics of the reference's fused GPU path.
+ *   EXACT    codes fed to bf16/fp16 MFMA exactly, each 32-deep block summed in fp32 and scaled by its fp32 d; fp32
+ *            activations are split into bf16 high and low parts. Tracks the reference's CPU float kernel.
+ *   INT8     activations quantized per row and 32-block to int8 exactly as the reference's integer kernel does,
+ *            int8 MFMA with int32 block sums, scales folded per block in fp32. Needs a workspace.
+ *   AUTO     DEQUANT for bf16/fp16 activations, EXACT for fp32. */
+enum { IDOLQ_MODE_AUTO = 0, IDOLQ_MODE_DEQUANT = 1, IDOLQ_MODE_EXACT = 2, IDOLQ_MODE_INT8 = 3 };
+
+/* GEMM flags. ROUND_BEFORE_BIAS rounds the product to the output dtype before the bias is added, as the reference's
+ * fused GPU path does (tools/idol_triton.py:84-89). */
+enum { IDOLQ_FLAG_ROUND_BEFORE_BIAS = 1 };
+
+enum {
+    IDOLQ_OK = 0,
+    IDOLQ_EINVAL = -1,  /* bad argument: shape, dtype, stride, alignment, size */
+    IDOLQ_ELAUNCH = -2, /* a HIP launch failed */
+    IDOLQ_ENOSUPPORT = -3
+};
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* idolq_last_error(void);
+
+/* Library version and the gfx target it was built for. */
+const char* idolq_version(void);
+
+/* Bytes of one Q8_0 weight of n rows and k columns: n * (k / 32) * 34 (0 when k % 32 != 0).
+ * Replaces the size check of tools/idol_triton.py:103-105 and tools/idol_packed.py:28-31. */
+int64_t idolq_q8_0_bytes(int64_t n, int64_t k);
+
+/* y[i, j] = epilogue( sum_k x[i, k] * w[n_offset + j, k] ) for i < m, j < n.
+ *   x        [m x k] in x_dtype, row stride ldx (>= k)
+ *   w        Q8_0 weight with n_total rows of k; only rows [n_offset, n_offset + n) are read
+ *   bias     NULL or n_total values in bias_dtype, indexed n_offset + j
+ *   residual NULL or [m x n] in residual_dtype, row stride ldr; may alias y (same dtype and stride)
+ *   act      IDOLQ_ACT_*, applied after bias and residual
+ *   y        [m x n] in y_dtype, row stride ldy
+ *   workspace / workspace_bytes  scratch for IDOLQ_MODE_INT8 (idolq_q8_0_gemm_workspace bytes), else may be NULL
+ * Replaces src/kernels.hpp:70-74 gemm_packed (fp32 x, residual before GELU, column window n_offset / n) and
+ * tools/idol_triton.py:94-126 fused_linear (bf16/fp16 x, bias after rounding: IDOLQ_FLAG_ROUND_BEFORE_BIAS). */
+int idolq_q8_0_gemm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* w, int64_t n_total,
+                    int64_t n_offset, int64_t n, const void* bias, int bias_dtype, const void* residual,
+                    int residual_dtype, int64_t ldr, int act, int mode, int flags, void* y, int y_dtype, int64_t ldy,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes idolq_q8_0_gemm needs for m rows of depth k in the given mode (0 except for IDOLQ_MODE_INT8). */
+size_t idolq_q8_0_gemm_workspace(int64_t m, int64_t k, int mode);
+
+/* Quantizes an fp32 [n x k] matrix (row stride ldw) to Q8_0 blocks: per 32 values d = amax / 127,
+ * q = round-half-away-from-zero(x * (1 / d)), d stored as fp16. The rule of ggml's quantize_row_q8_0_ref, which
+ * gguf-py's quantize(..., Q8_0) restates (tools/export_full_gguf.py:332-335, tests/python/test_fused_packed.py:40). */
+int idolq_q8_0_quantize(const float* w, int64_t n, int64_t k, int64_t ldw, uint8_t* out, void* stream);
+
+/* out[r, c] = out_dtype(fp32(d) * q) for the whole [n x k] weight, out row stride k.
+ * Replaces tools/idol_triton.py:24-33 _unpack_q8 and tools/idol_packed.py:25-31,71 PackedLinear.dequantize. */
+int idolq_q8_0_dequant(const uint8_t* w, int64_t n, int64_t k, void* out, int out_dtype, void* stream);
+
+/* Per row and 32-block of x [m x k]: amax, scale = amax / 127, inv = 127 / amax (0 when amax == 0),
+ * qa = round-to-nearest-even(x * inv) as int8, qsum = sum of qa. qa is [m x k], scale and qsum [m x k / 32].
+ * qsum may be NULL. Replaces src/kernels.cpp:368-404 quantize_activations (bit-exact). */
+int idolq_quantize_act_q8(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, int8_t* qa, float* scale,
+                          int32_t* qsum, void* stream);
+
+/* The int32 block dot products the INT8 GEMM computes with int8 MFMA, before any scaling:
+ * dots[(i * n + j) * (k / 32) + b] = sum_{t < 32} qa[i, 32 b + t] * q[n_offset + j, 32 b + t].
+ * A test entry point for the integer path of src/kernels.cpp:407-452 (vnni_task), whose sums are
+ * sum qa * (q + 128) = dots + 128 * qsum. */
+int idolq_q8_0_block_dots(const int8_t* qa, int64_t m, int64_t k, const uint8_t* w, int64_t n_total,
+                          int64_t n_offset, int64_t n, int32_t* dots, void* stream);
+
+/* Row-wise layer norm: y = (x - mean) / sqrt(var + eps), then * gamma + beta when gamma is given, then
+ * * (1 + scale[b]) + shift[b] when scale is given (adaLN), b = row / rows_per_batch (0 when rows_per_batch <= 0).
+ * Mean and variance are accumulated in fp64. gamma/beta are [dim] fp32; shift/scale are [batches x dim] fp32.
+ * y may alias x when the dtypes and strides match.
+ * Replaces src/decoders.cpp:23-42 norm_rows and src/kernels.cpp:599-618 layer_norm (eps 1e-5, gamma and beta). */
+int idolq_layernorm(const void* x, int x_dtype, int64_t rows, int64_t dim, int64_t ldx, float eps, const float* gamma,
+                    const float* beta, const float* shift, const float* scale, int64_t rows_per_batch, void* y,
+                    int y_dtype, int64_t ldy, void* stream);
+
+/* Non-causal multi-head attention, softmax(q k^T / sqrt(head_dim)) v per head and batch.
+ *   q  [batch][lq rows of stride ldq], head h at columns [h * head_dim, (h + 1) * head_dim), batch stride q_bs
+ *   k, v [batch][lk rows of stride ldkv], batch stride kv_bs
+ *   out  [batch][lq rows of stride ldo], batch stride o_bs
+ * q, k, v share `dtype`; out has out_dtype. bf16/fp16 inputs use MFMA (QK^T in the input type, fp32 online softmax,
+ * P and V in fp16 for P*V); fp32 inputs and head_dim other than 64 use an fp32 kernel.
+ * Replaces src/kernels.hpp:84-86 attention (batch 1, out stride dim). */
+int idolq_attention(const void* q, const void* k, const void* v, int dtype, int64_t batch, int64_t lq, int64_t lk,
+                    int64_t heads, int64_t head_dim, int64_t ldq, int64_t ldkv, int64_t q_bs, int64_t kv_bs, void* out,
+                    int out_dtype, int64_t ldo, int64_t o_bs, void* stream);
+
+/* In-place activation over count values: tanh-GELU (src/decoders.cpp:55-71 gelu_tanh), erf-GELU
+ * (src/kernels.cpp:826-850) or ReLU. */
+int idolq_activation(void* x, int dtype, int64_t count, int act, void* stream);
+
+/* Sine/cosine position embedding of 3-D coordinates (src/decoders.cpp:215-230 pos_embed, without the zero padding):
+ * out[r * ldo + c * 2 * nfreq + j] = sin((coords[r, c] * freqs[j]) * pi) and at + nfreq the cosine, for c < 3.
+ * coords [rows x 3] fp32, freqs [nfreq] fp32, out in out_dtype. */
+int idolq_pos_embed(const float* coords, int64_t rows, const float* freqs, int64_t nfreq, void* out, int out_dtype,
+                    int64_t ldo, void* stream);
+
+/* Copies a [rows x cols] block between dtypes and strides (a column slice of a wider row is a pointer offset). */
+int idolq_copy2d(const void* src, int src_dtype, int64_t lds, void* dst, int dst_dtype, int64_t ldd, int64_t rows,
+                 int64_t cols, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* IDOLQ_H */
