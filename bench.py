@@ -1,0 +1,208 @@
+"""Benchmark of the Q8_0 linear path on one MI355X.
+
+A step is one pass of the MLP block the metric is quoted on, on synthetic seeded data resident in HBM:
+    x bf16 [4096, 1536] ~ N(0, 1)
+    h = gelu_tanh(x @ W_up^T + b_up)      W_up   Q8_0 [6144 x 1536]  (bias and tanh-GELU fused in the epilogue)
+    y = h @ W_down^T + b_down + x         W_down Q8_0 [1536 x 6144]  (bias and residual fused in the epilogue)
+Weights ~ N(0, 0.02) and biases ~ N(0, 0.01), quantized to Q8_0 on the GPU. value = 2 * 2 * 4096 * 1536 * 6144 FLOP
+per step / measured time, in TFLOP/s.
+
+Also reported, in the same JSON line:
+  roofline       the GEMM kernel's average launch time from HIP events on its stream over the timed steps;
+                 achieved = 2 * M * N * K / launch time against the MFMA peak of the arithmetic it runs
+  pct_int8_peak  value as a fraction of the gfx950 dense int8 MFMA peak (5.0 POP/s), as the metric asks
+  denoiser_step_ms  one full synthetic denoiser step (24 layers, batch 2 x 4096 tokens), unless --no-denoiser
+  cpu_baseline   the reference's own CPU kernels (oracle/_ref, float kernel, all host cores) on the same MLP block
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "idol.cpp_amd"))
+
+METRIC = "Q8_0 GEMM TFLOP/s (% int8 MFMA peak) + denoiser-step ms at seq 4096, 1 GPU"
+PEAK_TFLOPS = {"bf16": 2500.0, "fp16": 2500.0, "int8": 5000.0}
+HBM_GBS = 8000.0
+M, D, H = 4096, 1536, 6144
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--mode", choices=["dequant", "exact", "int8"], default="dequant",
+                   help="GEMM arithmetic: bf16-dequant MFMA (the reference GPU path's numerics), exact-code bf16 "
+                        "MFMA with per-block fp32 scaling, or int8 MFMA on quantized activations")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-denoiser", action="store_true")
+    p.add_argument("--denoiser-layers", type=int, default=24)
+    p.add_argument("--cpu-rows", type=int, default=1024, help="rows of the MLP block the CPU baseline runs")
+    return p.parse_args()
+
+
+def mlp_inputs(torch, L, seed=0):
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    x = torch.randn((M, D), device="cuda", generator=gen).bfloat16()
+    w_up = L.quantize_q8_0(torch.randn((H, D), device="cuda", generator=gen) * 0.02)
+    w_down = L.quantize_q8_0(torch.randn((D, H), device="cuda", generator=gen) * 0.02)
+    b_up = torch.randn(H, device="cuda", generator=gen) * 0.01
+    b_down = torch.randn(D, device="cuda", generator=gen) * 0.01
+    return x, w_up, w_down, b_up, b_down
+
+
+def run_gpu(args):
+    import torch
+    import idolq_lib as L
+
+    mode = {"dequant": L.MODE_DEQUANT, "exact": L.MODE_EXACT, "int8": L.MODE_INT8}[args.mode]
+    x, w_up, w_down, b_up, b_down = mlp_inputs(torch, L)
+    h = torch.empty((M, H), device="cuda", dtype=torch.bfloat16)
+    y = torch.empty((M, D), device="cuda", dtype=torch.bfloat16)
+    ws = torch.empty(max(L.load().idolq_q8_0_gemm_workspace(M, H, mode), 16), device="cuda", dtype=torch.uint8)
+
+    def step(events=None):
+        if events is not None:
+            events[0].record()
+        L.gemm(x, w_up, H, bias=b_up, act=L.ACT_GELU_TANH, mode=mode, out=h, workspace=ws)
+        if events is not None:
+            events[1].record()
+        L.gemm(h, w_down, D, bias=b_down, residual=x, mode=mode, out=y, workspace=ws)
+        if events is not None:
+            events[2].record()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    # Events on the stream the kernels are launched on (torch's current stream, which idolq_lib passes down).
+    stream = torch.cuda.current_stream()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        for i in range(args.steps):
+            step(evs[i])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    up_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
+    down_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
+    flop_gemm = 2.0 * M * D * H
+    ms_per_step = elapsed * 1e3 / args.steps
+    value = 2 * flop_gemm / (ms_per_step * 1e-3) / 1e12
+    arith = {"dequant": "bf16", "exact": "bf16", "int8": "int8"}[args.mode]
+    gemm_ms = (up_ms + down_ms) / 2
+    achieved = flop_gemm / (gemm_ms * 1e-3) / 1e12
+    out = {
+        "value": value,
+        "ms_per_step": ms_per_step,
+        "dtype": arith,
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_TFLOPS[arith], "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_TFLOPS[arith], "traffic": None,
+                     "kernel": "q8_gemm_kernel" if args.mode != "int8" else "q8_gemm_int8_kernel",
+                     "launch_ms": {"up": up_ms, "down": down_ms},
+                     "flop_per_launch": flop_gemm},
+        "pct_int8_peak": value / PEAK_TFLOPS["int8"],
+    }
+    del h, y, ws
+    return out, (x, w_up, w_down, b_up, b_down)
+
+
+def run_denoiser(args):
+    import torch
+    import denoiser
+
+    model = denoiser.SyntheticDenoiser.build(layers=args.denoiser_layers, seed=0)
+    x, ctx = model.inputs(seed=1)
+    for _ in range(2):
+        model.step(x, ctx)
+    torch.cuda.synchronize()
+    reps = 5
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        model.step(x, ctx)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / reps
+    flop = model.flop_per_step()
+    return {"denoiser_step_ms": ms, "denoiser_tflops": flop / (ms * 1e-3) / 1e12,
+            "denoiser_layers": args.denoiser_layers}
+
+
+def run_cpu_baseline(args, inputs):
+    """The reference's kernels.cpp float kernel (oracle/_ref, all host cores) on args.cpu_rows rows of the block."""
+    import numpy as np
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle as O
+
+    x, w_up, w_down, b_up, b_down = inputs
+    rows = min(args.cpu_rows, M)
+    xs = x[:rows].float().cpu().numpy()
+    wu, wd = w_up.cpu().numpy(), w_down.cpu().numpy()
+    bu, bd = b_up.cpu().numpy(), b_down.cpu().numpy()
+    kind = "reference" if O.ref_available() else "port"
+    if kind == "reference":
+        blob_up, blob_down = O.q8_0_to_panel(wu, H, D), O.q8_0_to_panel(wd, D, H)
+
+        def block():
+            hh = O.ref_gemm_panel(xs, blob_up, bu, H, D, mode=0)
+            hh = O.ref_gelu_tanh(hh)
+            return O.ref_gemm_panel(hh, blob_down, bd, D, H, residual=xs, mode=0)
+    else:
+        def block():
+            hh = O.gelu_tanh(O.gemm_q8_float(xs, wu, H, D, bu))
+            return O.gemm_q8_float(hh, wd, D, H, bd, residual=xs)
+
+    block()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        block()
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    flop = 2 * 2.0 * rows * D * H
+    cores = int(os.environ.get("OMP_NUM_THREADS", 0)) or os.cpu_count()
+    return {"value": flop / t / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": kind,
+            "sample": f"MLP block (up + tanh-GELU + down + residual) on {rows} of {M} rows, fp32, float kernel "
+                      f"(IDOL_QUANT_KERNEL=float), median of 3 after 1 warm-up, {t * 1e3:.1f} ms per block"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py runs on exactly one GPU: this build has no multi-GPU path (--gpus must be 1)", file=sys.stderr)
+        sys.exit(2)
+    gpu, inputs = run_gpu(args)
+    result = {
+        "metric": METRIC,
+        "value": round(gpu["value"], 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(gpu["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": gpu["dtype"],
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights quantized to Q8_0, N(0,0.01) biases)",
+        "config": {"workload": "Q8_0 MLP block: x bf16 [4096,1536] -> up Q8_0 [6144x1536] + bias + tanh-GELU -> "
+                               "down Q8_0 [1536x6144] + bias + residual",
+                   "m": M, "k_up": D, "n_up": H, "gemm_mode": args.mode},
+        "roofline": gpu["roofline"],
+        "pct_int8_peak": round(gpu["pct_int8_peak"], 4),
+    }
+    if not args.no_denoiser:
+        try:
+            result.update(run_denoiser(args))
+        except ImportError:
+            result["denoiser_step_ms"] = None
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = run_cpu_baseline(args, inputs)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -254,7 +254,6 @@ using namespace idolq;
 extern "C" int idolq_attention(const void* q, const void* k, const void* v, int dtype, int64_t batch, int64_t lq,
                                int64_t lk, int64_t heads, int64_t head_dim, int64_t ldq, int64_t ldkv, int64_t q_bs,
                                int64_t kv_bs, void* out, int out_dtype, int64_t ldo, int64_t o_bs, void* stream) {
-    if (!q || !k || !v || !out) return fail(IDOLQ_EINVAL, "q, k, v and out must be non-null");
     if (!dtype_ok(dtype) || !dtype_ok(out_dtype)) return fail(IDOLQ_EINVAL, "unknown dtype code");
     if (batch < 0 || lq < 0 || lk <= 0 || heads <= 0 || head_dim <= 0 || head_dim > kMaxHD)
         return fail(IDOLQ_EINVAL, "bad attention shape (needs lk > 0 and 0 < head_dim <= 256)");
@@ -262,6 +261,7 @@ extern "C" int idolq_attention(const void* q, const void* k, const void* v, int 
     if (ldq < dim || ldkv < dim || ldo < dim) return fail(IDOLQ_EINVAL, "row stride smaller than heads * head_dim");
     if (batch > 65535 || heads > 65535 || lq > 0x7fffffff) return fail(IDOLQ_EINVAL, "grid too large");
     if (batch == 0 || lq == 0) return IDOLQ_OK;
+    if (!q || !k || !v || !out) return fail(IDOLQ_EINVAL, "q, k, v and out must be non-null");
     AttnParams p{q, k, v, out, dtype, out_dtype, lq, lk, heads, head_dim, ldq, ldkv, q_bs, kv_bs, ldo, o_bs,
                  1.4426950408889634f / sqrtf((float)head_dim)};
     hipStream_t s = static_cast<hipStream_t>(stream);

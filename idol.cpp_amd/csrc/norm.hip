@@ -90,9 +90,10 @@ using namespace idolq;
 extern "C" int idolq_layernorm(const void* x, int x_dtype, int64_t rows, int64_t dim, int64_t ldx, float eps,
                                const float* gamma, const float* beta, const float* shift, const float* scale,
                                int64_t rows_per_batch, void* y, int y_dtype, int64_t ldy, void* stream) {
-    if (!x || !y) return fail(IDOLQ_EINVAL, "x and y must be non-null");
     if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype)) return fail(IDOLQ_EINVAL, "unknown dtype code");
     if (rows < 0 || dim <= 0 || ldx < dim || ldy < dim) return fail(IDOLQ_EINVAL, "bad layer norm shape");
+    if (rows == 0) return IDOLQ_OK;
+    if (!x || !y) return fail(IDOLQ_EINVAL, "x and y must be non-null");
     if (x == y && (x_dtype != y_dtype || ldx != ldy)) return fail(IDOLQ_EINVAL, "in place needs equal dtypes and strides");
     if ((shift == nullptr) != (scale == nullptr)) return fail(IDOLQ_EINVAL, "adaLN needs both shift and scale");
     if (rows == 0) return IDOLQ_OK;

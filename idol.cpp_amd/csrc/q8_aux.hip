@@ -181,22 +181,22 @@ extern "C" int64_t idolq_q8_0_bytes(int64_t n, int64_t k) {
 }
 
 extern "C" int idolq_q8_0_dequant(const uint8_t* w, int64_t n, int64_t k, void* out, int out_dtype, void* stream) {
-    if (!w || !out) return fail(IDOLQ_EINVAL, "w and out must be non-null");
     if (!dtype_ok(out_dtype)) return fail(IDOLQ_EINVAL, "unknown dtype code");
     if (n < 0 || k <= 0 || k % kQ8Block) return fail(IDOLQ_EINVAL, "need n >= 0 and k a positive multiple of 32");
-    if (reinterpret_cast<uintptr_t>(out) % 16 != 0) return fail(IDOLQ_EINVAL, "out must be 16-byte aligned");
     const int64_t blocks = n * (k / kQ8Block);
     if (blocks == 0) return IDOLQ_OK;
+    if (!w || !out) return fail(IDOLQ_EINVAL, "w and out must be non-null");
+    if (reinterpret_cast<uintptr_t>(out) % 16 != 0) return fail(IDOLQ_EINVAL, "out must be 16-byte aligned");
     hipLaunchKernelGGL(q8_dequant_kernel, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), w, blocks, out, out_dtype);
     return check_launch("q8_dequant_kernel");
 }
 
 extern "C" int idolq_q8_0_quantize(const float* w, int64_t n, int64_t k, int64_t ldw, uint8_t* out, void* stream) {
-    if (!w || !out) return fail(IDOLQ_EINVAL, "w and out must be non-null");
     if (n < 0 || k <= 0 || k % kQ8Block || ldw < k) return fail(IDOLQ_EINVAL, "need n >= 0, k a positive multiple of 32, ldw >= k");
     const int64_t nb = k / kQ8Block, blocks = n * nb;
     if (blocks == 0) return IDOLQ_OK;
+    if (!w || !out) return fail(IDOLQ_EINVAL, "w and out must be non-null");
     hipLaunchKernelGGL(q8_quantize_kernel, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), w, nb, blocks, ldw, out);
     return check_launch("q8_quantize_kernel");
@@ -204,9 +204,10 @@ extern "C" int idolq_q8_0_quantize(const float* w, int64_t n, int64_t k, int64_t
 
 extern "C" int idolq_quantize_act_q8(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, int8_t* qa,
                                      float* scale, int32_t* qsum, void* stream) {
-    if (!x || !qa || !scale) return fail(IDOLQ_EINVAL, "x, qa and scale must be non-null");
     if (!dtype_ok(x_dtype)) return fail(IDOLQ_EINVAL, "unknown dtype code");
     if (m < 0 || k <= 0 || k % kQ8Block || ldx < k) return fail(IDOLQ_EINVAL, "need m >= 0, k a positive multiple of 32, ldx >= k");
+    if (m == 0) return IDOLQ_OK;
+    if (!x || !qa || !scale) return fail(IDOLQ_EINVAL, "x, qa and scale must be non-null");
     if (reinterpret_cast<uintptr_t>(qa) % 16 != 0) return fail(IDOLQ_EINVAL, "qa must be 16-byte aligned");
     return quantize_act_launch(x, x_dtype, m, k, ldx, qa, scale, qsum, static_cast<hipStream_t>(stream));
 }
@@ -223,10 +224,10 @@ extern "C" int idolq_activation(void* x, int dtype, int64_t count, int act, void
 
 extern "C" int idolq_pos_embed(const float* coords, int64_t rows, const float* freqs, int64_t nfreq, void* out,
                                int out_dtype, int64_t ldo, void* stream) {
-    if (!coords || !freqs || !out) return fail(IDOLQ_EINVAL, "coords, freqs and out must be non-null");
     if (!dtype_ok(out_dtype)) return fail(IDOLQ_EINVAL, "unknown dtype code");
     if (rows < 0 || nfreq <= 0 || nfreq > 65536 || ldo < 6 * nfreq) return fail(IDOLQ_EINVAL, "bad pos_embed shape");
     if (rows == 0) return IDOLQ_OK;
+    if (!coords || !freqs || !out) return fail(IDOLQ_EINVAL, "coords, freqs and out must be non-null");
     const int64_t items = rows * 3 * nfreq;
     hipLaunchKernelGGL(pos_embed_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), coords, rows, freqs, (int)nfreq, out, out_dtype, ldo);
@@ -235,10 +236,10 @@ extern "C" int idolq_pos_embed(const float* coords, int64_t rows, const float* f
 
 extern "C" int idolq_copy2d(const void* src, int src_dtype, int64_t lds, void* dst, int dst_dtype, int64_t ldd,
                             int64_t rows, int64_t cols, void* stream) {
-    if (!src || !dst) return fail(IDOLQ_EINVAL, "src and dst must be non-null");
     if (!dtype_ok(src_dtype) || !dtype_ok(dst_dtype)) return fail(IDOLQ_EINVAL, "unknown dtype code");
     if (rows < 0 || cols < 0 || lds < cols || ldd < cols) return fail(IDOLQ_EINVAL, "bad copy shape");
     if (rows * cols == 0) return IDOLQ_OK;
+    if (!src || !dst) return fail(IDOLQ_EINVAL, "src and dst must be non-null");
     hipLaunchKernelGGL(copy2d_kernel, dim3(grid_for(rows * cols)), dim3(256), 0, static_cast<hipStream_t>(stream), src,
                        src_dtype, lds, dst, dst_dtype, ldd, rows, cols);
     return check_launch("copy2d_kernel");

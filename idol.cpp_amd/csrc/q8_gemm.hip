@@ -531,7 +531,6 @@ extern "C" int idolq_q8_0_gemm(const void* x, int x_dtype, int64_t m, int64_t k,
                                const void* residual, int residual_dtype, int64_t ldr, int act, int mode, int flags,
                                void* y, int y_dtype, int64_t ldy, void* workspace, size_t workspace_bytes,
                                void* stream) {
-    if (!x || !w || !y) return fail(IDOLQ_EINVAL, "x, w and y must be non-null");
     if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype) || (bias && !dtype_ok(bias_dtype)) ||
         (residual && !dtype_ok(residual_dtype)))
         return fail(IDOLQ_EINVAL, "unknown dtype code");
@@ -547,7 +546,8 @@ extern "C" int idolq_q8_0_gemm(const void* x, int x_dtype, int64_t m, int64_t k,
     if (mode < IDOLQ_MODE_DEQUANT || mode > IDOLQ_MODE_INT8) return fail(IDOLQ_EINVAL, "unknown GEMM mode");
     if (mode == IDOLQ_MODE_DEQUANT && x_dtype == IDOLQ_F32)
         return fail(IDOLQ_EINVAL, "DEQUANT mode takes bf16 or fp16 activations");
-    if (m == 0 || n == 0) return IDOLQ_OK;
+    if (m == 0 || n == 0) return IDOLQ_OK;  // empty input: nothing to read or write (pointers may be null)
+    if (!x || !w || !y) return fail(IDOLQ_EINVAL, "x, w and y must be non-null");
     hipStream_t s = static_cast<hipStream_t>(stream);
 
     GemmParams p{};
@@ -591,9 +591,10 @@ extern "C" int idolq_q8_0_gemm(const void* x, int x_dtype, int64_t m, int64_t k,
 
 extern "C" int idolq_q8_0_block_dots(const int8_t* qa, int64_t m, int64_t k, const uint8_t* w, int64_t n_total,
                                      int64_t n_offset, int64_t n, int32_t* dots, void* stream) {
-    if (!qa || !w || !dots) return fail(IDOLQ_EINVAL, "qa, w and dots must be non-null");
     if (m < 0 || n < 0 || k <= 0 || k % kQ8Block) return fail(IDOLQ_EINVAL, "need m >= 0, n >= 0 and k a positive multiple of 32");
     if (n_offset < 0 || n_offset + n > n_total) return fail(IDOLQ_EINVAL, "column window outside the weight rows");
+    if (m == 0 || n == 0) return IDOLQ_OK;
+    if (!qa || !w || !dots) return fail(IDOLQ_EINVAL, "qa, w and dots must be non-null");
     if (reinterpret_cast<uintptr_t>(qa) % 16 != 0 || k % 16 != 0) return fail(IDOLQ_EINVAL, "qa must be 16-byte aligned");
     if ((reinterpret_cast<uintptr_t>(w) & 1) != 0) return fail(IDOLQ_EINVAL, "Q8_0 weights must be 2-byte aligned");
     if (m == 0 || n == 0) return IDOLQ_OK;

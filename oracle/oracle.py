@@ -208,6 +208,8 @@ def attention(q, k, v, lq, lk, ldq, ldkv, heads, head_dim):
     """q, k, v are flat fp32 buffers of lq * ldq and lk * ldkv values. Returns [lq, heads * head_dim]."""
     q, k, v = _f32(q), _f32(k), _f32(v)
     dim = heads * head_dim
+    if q.size < (lq - 1) * ldq + dim or k.size < (lk - 1) * ldkv + dim or v.size < (lk - 1) * ldkv + dim:
+        raise ValueError("attention buffers are smaller than their rows and strides")
     out = np.empty((lq, dim), np.float32)
     oracle_lib().orc_attention(_ptr(q), lq, ldq, _ptr(k), _ptr(v), lk, ldkv, heads, head_dim, out, dim)
     return out

@@ -1,0 +1,129 @@
+"""GPU parity of the kernels between the GEMMs: layer norm (plain, affine, adaLN, in place), attention (MFMA and
+fp32 kernels), activations and the position embedding, against the oracle and the reference's golden vectors."""
+import numpy as np
+import pytest
+import torch
+
+import idolq_lib as L
+import oracle as O
+from conftest import norm_rel
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def to_dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def test_layer_norm_matches_reference_golden(golden):
+    # fp64 accumulation as the reference's norm_rows: bit-identical except, rarely, one ulp (1e-6 abs bar)
+    g = golden("norm")
+    x = to_dev(g["x"])
+    cases = [
+        (L.layernorm(to_dev(g["small"]), 1e-5, gamma=to_dev(g["g24"]), beta=to_dev(g["b24"])), g["layer_norm_small"]),
+        (L.layernorm(x, 1e-5, gamma=to_dev(g["gamma"]), beta=to_dev(g["beta"])), g["layer_norm"]),
+        (L.layernorm(x, 1e-6), g["norm_plain"]),
+        (L.layernorm(x, 1e-6, gamma=to_dev(g["gamma"]), beta=to_dev(g["beta"])), g["norm_affine"]),
+        (L.layernorm(x, 1e-6, shift=to_dev(g["shift"]), scale=to_dev(g["scale"])), g["norm_ada"]),
+        (L.layernorm(x, 1e-5), g["norm_eps5"]),
+    ]
+    for got, ref in cases:
+        assert np.max(np.abs(got.cpu().numpy() - ref)) < 1e-5
+
+
+def test_adaln_batches_in_place_and_bf16():
+    rng = np.random.default_rng(20)
+    rows, dim = 2 * 300, 1536
+    x = rng.normal(0.2, 1.5, (rows, dim)).astype(np.float32)
+    sh = rng.normal(0, 0.1, (2, dim)).astype(np.float32)
+    sc = rng.normal(0, 0.1, (2, dim)).astype(np.float32)
+    ref = O.norm_rows(x, 1e-6, shift=sh, scale=sc, rows_per_batch=300)
+    xt = to_dev(x)
+    L.layernorm(xt, 1e-6, shift=to_dev(sh), scale=to_dev(sc), rows_per_batch=300, out=xt)  # in place
+    assert np.max(np.abs(xt.cpu().numpy() - ref)) < 1e-5
+    xb = to_dev(x).bfloat16()
+    yb = L.layernorm(xb, 1e-6, shift=to_dev(sh), scale=to_dev(sc), rows_per_batch=300)
+    refb = O.norm_rows(xb.float().cpu().numpy(), 1e-6, shift=sh, scale=sc, rows_per_batch=300)
+    assert norm_rel(yb.float().cpu().numpy(), torch.from_numpy(refb).bfloat16().float().numpy()) < 1e-3
+    # dims above the register-resident limit take the re-reading path
+    x2 = rng.normal(0, 1, (5, 6144)).astype(np.float32)
+    assert np.max(np.abs(L.layernorm(to_dev(x2), 1e-6).cpu().numpy() - O.norm_rows(x2, 1e-6))) < 1e-5
+
+
+def test_attention_fp32_matches_reference_golden(golden):
+    # the reference test shapes, strided rows (tests/test_kernels.cpp:184-228); fp32 kernel, 1e-5 norm-relative
+    g = golden("attention")
+    for i in range(int(g["cases"])):
+        lq, lk, heads, hd, ldq, ldkv = (int(v) for v in g[f"c{i}_shape"])
+        dim = heads * hd
+        out = torch.empty((lq, dim), device=DEV)
+        L.attention(to_dev(g[f"c{i}_q"]), to_dev(g[f"c{i}_k"]), to_dev(g[f"c{i}_v"]), 1, lq, lk, heads, hd, ldq,
+                    ldkv, 0, 0, out, dim, 0)
+        assert norm_rel(out.cpu().numpy(), g[f"c{i}_out"]) < 1e-5, i
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("lq,lk,heads", [(130, 77, 2), (256, 256, 3), (1, 1, 1), (128, 1024, 2), (300, 64, 1)])
+def test_attention_mfma_tracks_fp32_attention(dtype, lq, lk, heads):
+    # 16-bit inputs, head_dim 64: against the oracle on the upcast inputs, output rounded to the input dtype, 1e-3
+    rng = np.random.default_rng(21)
+    hd, dim = 64, heads * 64
+    q = to_dev(rng.normal(0, 1, (lq, dim)).astype(np.float32)).to(dtype)
+    k = to_dev(rng.normal(0, 1, (lk, dim)).astype(np.float32)).to(dtype)
+    v = to_dev(rng.normal(0, 1, (lk, dim)).astype(np.float32)).to(dtype)
+    out = torch.empty((lq, dim), device=DEV, dtype=dtype)
+    L.attention(q, k, v, 1, lq, lk, heads, hd, dim, dim, 0, 0, out, dim, 0)
+    ref = O.attention(q.float().cpu().numpy(), k.float().cpu().numpy(), v.float().cpu().numpy(), lq, lk, dim, dim,
+                      heads, hd)
+    assert norm_rel(out.float().cpu().numpy(), torch.from_numpy(ref).to(dtype).float().numpy()) < 1e-3
+
+
+def test_attention_batched_strided_views_of_a_qkv_buffer():
+    # batch 2 (guidance pairs), q/k/v as column slices of one [B*S, 3*D] projection buffer, out written strided
+    rng = np.random.default_rng(22)
+    B, S, heads, hd = 2, 200, 3, 64
+    D = heads * hd
+    qkv = to_dev(rng.normal(0, 1, (B * S, 3 * D)).astype(np.float32)).bfloat16()
+    out = torch.zeros((B * S, D + 8), device=DEV, dtype=torch.bfloat16)
+    L.attention(qkv[:, :D], qkv[:, D:2 * D], qkv[:, 2 * D:], B, S, S, heads, hd, 3 * D, 3 * D, S * 3 * D, S * 3 * D,
+                out, D + 8, S * (D + 8))
+    host = qkv.float().cpu().numpy()
+    for b in range(B):
+        blk = host[b * S:(b + 1) * S]
+        ref = O.attention(blk[:, :D], blk[:, D:2 * D], blk[:, 2 * D:], S, S, D, D, heads, hd)
+        got = out[b * S:(b + 1) * S, :D].float().cpu().numpy()
+        assert norm_rel(got, torch.from_numpy(ref).bfloat16().float().numpy()) < 1e-3
+    assert not out[:, D:].any()
+
+
+def test_cross_attention_shape_sample():
+    # cross-attention: 4096 queries against 1024 context tokens, 24 heads of 64, on a 256-query sample for the oracle
+    rng = np.random.default_rng(23)
+    lq, lk, heads, hd = 4096, 1024, 24, 64
+    D = heads * hd
+    q = to_dev(rng.normal(0, 1, (lq, D)).astype(np.float32)).bfloat16()
+    kv = to_dev(rng.normal(0, 1, (lk, 2 * D)).astype(np.float32)).bfloat16()
+    out = torch.empty((lq, D), device=DEV, dtype=torch.bfloat16)
+    L.attention(q, kv[:, :D], kv[:, D:], 1, lq, lk, heads, hd, D, 2 * D, 0, 0, out, D, 0)
+    rows = np.arange(0, lq, 16)
+    kvh = kv.float().cpu().numpy()
+    ref = O.attention(q.float().cpu().numpy()[rows], kvh[:, :D], kvh[:, D:], len(rows), lk, D, D, heads, hd)
+    assert norm_rel(out[rows].float().cpu().numpy(), torch.from_numpy(ref).bfloat16().float().numpy()) < 1e-3
+
+
+def test_activations_and_position_embedding(golden):
+    g = golden("elementwise")
+    xt = to_dev(g["x_tanh"].copy())
+    L.activation(xt, L.ACT_GELU_TANH)
+    assert np.max(np.abs(xt.cpu().numpy() - g["gelu_tanh"])) < 1e-5
+    xg = to_dev(g["x_gelu"].copy())
+    L.activation(xg, L.ACT_GELU_ERF)
+    assert np.max(np.abs(xg.cpu().numpy() - g["gelu256"])) < 2e-6
+    freqs = (2.0 ** np.linspace(0, 10, 16)).astype(np.float32)
+    coords = np.random.default_rng(24).uniform(-1, 1, (1000, 3)).astype(np.float32)
+    out = torch.zeros((1000, 352), device=DEV)
+    L.pos_embed(to_dev(coords), to_dev(freqs), out[:, 256:])
+    ref = O.pos_embed(freqs, coords)
+    got = out.cpu().numpy()
+    assert np.max(np.abs(got[:, 256:] - ref)) < 1e-4 and not got[:, :256].any()
