@@ -25,7 +25,6 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kKStep = 64;                // depth per stage: two Q8_0 blocks
 constexpr int kAPitch = kKStep + 8;       // 16-bit elements per activation row in LDS (144 bytes)
-constexpr int kCodePitch = kKStep + 8;    // bytes per weight row of codes in LDS for 8-byte reads (72)
 constexpr int kCodePitch8 = kKStep + 16;  // bytes per row of int8 operands for 16-byte reads (80)
 
 enum { XT_BF16 = 0, XT_F16 = 1, XT_F32 = 2 };
@@ -48,6 +47,7 @@ struct GemmParams {
     int act, flags;
     int tiles_m, tiles_n;
     int x_aligned;  // x rows are 16-byte aligned
+    int y_vec;      // y (and the residual, when given) rows and base are 16-byte aligned: vector epilogue stores
     // INT8 mode
     const int8_t* qa;
     const float* sa;
@@ -143,30 +143,50 @@ struct WeightStage {
 };
 
 // ------------------------------------------------------------------------------------------------ activation staging
-// BM rows x 64 k of x per stage, 16 bytes per unit.
-template <int BM, int XT>
+// BM rows x 64 k of x per stage in 16-byte units. The per-thread row offsets (in 16-byte units, ~0u for rows
+// outside m) are computed once; a stage only adds its k offset. Unit u = tid + 256 i covers row u / kUnitsPerRow,
+// column unit tid % kUnitsPerRow (the same for every i).
+template <int BM, int XT, int THREADS>
 struct ActStage {
     static constexpr int kEsz = XT == XT_F32 ? 4 : 2;
     static constexpr int kUnitsPerRow = kKStep * kEsz / 16;  // 8 (16-bit) or 16 (fp32)
-    static constexpr int kUnits = BM * kUnitsPerRow;
-    static constexpr int kPer = kUnits / kThreads;
-    static_assert(kUnits % kThreads == 0, "tile size");
+    static constexpr int kRowsPerPass = THREADS / kUnitsPerRow;
+    static constexpr int kPer = BM / kRowsPerPass;
+    static constexpr int kElems = 16 / kEsz;
+    static_assert(BM % kRowsPerPass == 0, "tile size");
+    uint32_t off[kPer];  // element offset of the unit's row start + column unit, ~0u when the row is outside m
     uint4 v[kPer];
 
-    __device__ __forceinline__ void load(const GemmParams& p, int m0, int k0) {
-        const int tid = threadIdx.x;
-        constexpr int kElems = 16 / kEsz;
+    __device__ __forceinline__ void init(const GemmParams& p, int m0) {
+        const int cu = threadIdx.x % kUnitsPerRow, r0 = threadIdx.x / kUnitsPerRow;
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
-            const int u = tid + i * kThreads;
-            const int row = u / kUnitsPerRow, cu = u - row * kUnitsPerRow;
-            const int kk = k0 + cu * kElems;
+            const int row = m0 + r0 + i * kRowsPerPass;
+            off[i] = row < p.m ? (uint32_t)((int64_t)row * p.ldx + cu * kElems) : ~0u;
+        }
+    }
+
+    // Invalid units (rows outside m, depth beyond k) read the first element of x and are zeroed by a select, so the
+    // loads need no branches.
+    __device__ __forceinline__ void load(const GemmParams& p, int k0) {
+        const int kk = k0 + (threadIdx.x % kUnitsPerRow) * kElems;
+        const bool kin = kk < p.k;
+        if (p.x_aligned) {
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) {
+                const bool ok = off[i] != ~0u && kin;
+                const char* src = static_cast<const char*>(p.x) + (ok ? ((size_t)off[i] + k0) * kEsz : 0);
+                const uint4 t = *reinterpret_cast<const uint4*>(src);
+                v[i] = ok ? t : make_uint4(0, 0, 0, 0);
+            }
+            return;
+        }
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
             v[i] = make_uint4(0, 0, 0, 0);
-            if (m0 + row < p.m && kk < p.k) {
-                const char* src = static_cast<const char*>(p.x) + ((int64_t)(m0 + row) * p.ldx + kk) * kEsz;
-                if (p.x_aligned) {
-                    v[i] = *reinterpret_cast<const uint4*>(src);
-                } else {
+            if (off[i] != ~0u && kin) {
+                const char* src = static_cast<const char*>(p.x) + ((size_t)off[i] + k0) * kEsz;
+                {
                     uint32_t t[4];
                     if (kEsz == 4) {
 #pragma unroll
@@ -184,15 +204,12 @@ struct ActStage {
 
     // hi (and, for fp32 input, lo) tiles [BM][kAPitch] of 16-bit MFMA operands.
     __device__ __forceinline__ void store(uint16_t* hi, uint16_t* lo) const {
-        const int tid = threadIdx.x;
-        constexpr int kElems = 16 / kEsz;
+        const int cu = threadIdx.x % kUnitsPerRow, r0 = threadIdx.x / kUnitsPerRow;
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
-            const int u = tid + i * kThreads;
-            const int row = u / kUnitsPerRow, cu = u - row * kUnitsPerRow;
-            const int off = row * kAPitch + cu * kElems;
+            const int off_lds = (r0 + i * kRowsPerPass) * kAPitch + cu * kElems;
             if (XT != XT_F32) {
-                *reinterpret_cast<uint4*>(hi + off) = v[i];
+                *reinterpret_cast<uint4*>(hi + off_lds) = v[i];
             } else {
                 const float f[4] = {__builtin_bit_cast(float, v[i].x), __builtin_bit_cast(float, v[i].y),
                                     __builtin_bit_cast(float, v[i].z), __builtin_bit_cast(float, v[i].w)};
@@ -205,8 +222,58 @@ struct ActStage {
                     h[e] = (uint32_t)h0 | ((uint32_t)h1 << 16);
                     l[e] = (uint32_t)l0 | ((uint32_t)l1 << 16);
                 }
-                *reinterpret_cast<uint2*>(hi + off) = make_uint2(h[0], h[1]);
-                *reinterpret_cast<uint2*>(lo + off) = make_uint2(l[0], l[1]);
+                *reinterpret_cast<uint2*>(hi + off_lds) = make_uint2(h[0], h[1]);
+                *reinterpret_cast<uint2*>(lo + off_lds) = make_uint2(l[0], l[1]);
+            }
+        }
+    }
+};
+
+// ------------------------------------------------------------------------------------------------ raw weight staging
+// The 68 bytes (two Q8_0 blocks) of each of BN weight rows per stage, copied unchanged into LDS as a [BN][68-byte]
+// array: dword (W4) or halfword unit u of the flat run is row u / 17 (u / 34), and it lands at LDS unit u, so the
+// global reads are one coalesced run per row and the LDS writes one contiguous run per wave.
+template <int BN, bool W4, int THREADS>
+struct RawStage {
+    static constexpr int kUnitsPerRow = W4 ? 17 : 34;
+    static constexpr int kUnits = BN * kUnitsPerRow;
+    static constexpr int kPer = (kUnits + THREADS - 1) / THREADS;
+    uint32_t off[kPer];  // byte offset of the unit within the window (row * row_bytes + part * size), ~0u if unused
+    bool second[kPer];   // the unit belongs to the second block of the stage
+    uint32_t v[kPer];
+
+    __device__ __forceinline__ void init(const GemmParams& p, int n0) {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int u = threadIdx.x + i * THREADS;
+            const int row = u / kUnitsPerRow, part = u - row * kUnitsPerRow;
+            off[i] = (u < kUnits && n0 + row < p.n) ? (uint32_t)((int64_t)(n0 + row) * p.row_bytes + part * (W4 ? 4 : 2))
+                                                    : ~0u;
+            second[i] = W4 ? part >= 9 : part >= 17;
+        }
+    }
+
+    // Units outside the window (or in a missing second block) read the window's first bytes and are zeroed.
+    __device__ __forceinline__ void load(const GemmParams& p, int blk0, int nblocks) {
+        const bool has_second = blk0 + 1 < nblocks;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const bool ok = off[i] != ~0u && (has_second || !second[i]);
+            const uint8_t* src = p.w + (ok ? off[i] + (size_t)blk0 * kQ8Bytes : 0);
+            const uint32_t t = W4 ? *reinterpret_cast<const uint32_t*>(src) : (uint32_t) * reinterpret_cast<const uint16_t*>(src);
+            v[i] = ok ? t : 0u;
+        }
+    }
+
+    __device__ __forceinline__ void store(uint32_t* raw) const {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int u = threadIdx.x + i * THREADS;
+            if (u < kUnits) {
+                if (W4)
+                    raw[u] = v[i];
+                else
+                    reinterpret_cast<uint16_t*>(raw)[u] = (uint16_t)v[i];
             }
         }
     }
@@ -232,18 +299,71 @@ struct Mfma<_Float16> {
     }
 };
 
-// Eight int8 codes (in a uint2) to an MFMA operand: exact codes, or T(fp32(d) * q).
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Eight int8 codes (in a uint2) to eight 16-bit operand values: exact codes, or T(fp32(d) * q). Pairs are rounded
+// together (one v_cvt_pk_bf16_f32 for bf16).
 template <typename T, int MODE>
-__device__ __forceinline__ typename Mfma<T>::vec codes_to_operand(uint2 raw, float d) {
-    typename Mfma<T>::vec out;
+__device__ __forceinline__ uint4 codes_to_operand(uint2 raw, float d) {
+    typedef typename std::conditional<std::is_same<T, __bf16>::value, bf16x2, f16x2>::type T2;
+    uint32_t out[4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const uint32_t word = e < 4 ? raw.x : raw.y;
-        const int q = (int)(int8_t)(uint8_t)(word >> (8 * (e & 3)));
-        const float f = MODE == MODE_DEQUANT ? (float)q * d : (float)q;
-        out[e] = static_cast<T>(f);
+    for (int e = 0; e < 4; ++e) {
+        const uint32_t word = e < 2 ? raw.x : raw.y;
+        const int sh = 16 * (e & 1);
+        f32x2 f;
+        f.x = (float)(int)(int8_t)(uint8_t)(word >> sh);
+        f.y = (float)(int)(int8_t)(uint8_t)(word >> (sh + 8));
+        if (MODE == MODE_DEQUANT) f = f * d;
+        out[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, T2));
     }
-    return out;
+    return make_uint4(out[0], out[1], out[2], out[3]);
+}
+
+// Converts the raw [BN][68-byte] stage into 16-bit B operands [BN][kAPitch] (and, for EXACT, fp32 scales [BN][2]).
+// Thread t handles row t / 2 (+128 per pass) and the four 8-code chunks (blk, jj = 2 q + t % 2): block 0's codes sit
+// at byte 2 + 8 jj (two bytes off dword alignment, realigned with alignbyte), block 1's at byte 36 + 8 jj.
+// All LDS reads of a pass are issued before any of its arithmetic, so their latency is paid once.
+template <typename T, int BN, int MODE, int THREADS>
+__device__ __forceinline__ void convert_stage(const uint32_t* raw, uint16_t* b, float* bscale) {
+    constexpr int kRows = THREADS / 2;  // rows per pass: two threads per row
+    const int half = threadIdx.x & 1;
+#pragma unroll
+    for (int rp = 0; rp < (BN + kRows - 1) / kRows; ++rp) {
+        const int row = rp * kRows + (threadIdx.x >> 1);
+        if (BN % kRows != 0 && row >= BN) break;
+        const uint32_t* rw = raw + row * 17;
+        // dwords 2jj..2jj+2 (block 0) and 9+2jj, 10+2jj (block 1) for jj = half and 2 + half; dword 0 and 8 scales
+        uint32_t w[12];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int jj = 2 * q + half;
+            w[6 * q + 0] = rw[2 * jj];
+            w[6 * q + 1] = rw[2 * jj + 1];
+            w[6 * q + 2] = rw[2 * jj + 2];
+            w[6 * q + 3] = rw[9 + 2 * jj];
+            w[6 * q + 4] = rw[10 + 2 * jj];
+        }
+        const uint32_t s0 = rw[0], s8 = rw[8];
+        const float d0 = half_bits_to_float((uint16_t)(s0 & 0xffff));
+        const float d1 = half_bits_to_float((uint16_t)(s8 >> 16));
+        if (MODE == MODE_EXACT && half == 0) {
+            bscale[row * 2] = d0;
+            bscale[row * 2 + 1] = d1;
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int jj = 2 * q + half;
+            const uint2 c0 = make_uint2(__builtin_amdgcn_alignbyte(w[6 * q + 1], w[6 * q + 0], 2),
+                                        __builtin_amdgcn_alignbyte(w[6 * q + 2], w[6 * q + 1], 2));
+            const uint4 o0 = codes_to_operand<T, MODE>(c0, d0);
+            const uint4 o1 = codes_to_operand<T, MODE>(make_uint2(w[6 * q + 3], w[6 * q + 4]), d1);
+            *reinterpret_cast<uint4*>(b + row * kAPitch + 8 * jj) = o0;
+            *reinterpret_cast<uint4*>(b + row * kAPitch + 32 + 8 * jj) = o1;
+        }
+    }
 }
 
 // ------------------------------------------------------------------------------------------------ epilogue
@@ -274,17 +394,114 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, const f32x16 (&a
     }
 }
 
+
+// Epilogue through LDS: the accumulator tile is written to LDS as fp32 ([BM][BN + 4]), then each thread takes runs of
+// 8 consecutive columns of one row and applies the epilogue with vector loads of bias and residual and one 16-byte
+// (32-byte for fp32) store per run, so each wave writes whole row segments instead of 2-byte scattered stores.
+template <int BM, int BN, int TM, int TN, int WM, int WN, int THREADS>
+__device__ __forceinline__ void write_tile_staged(const GemmParams& p, const f32x16 (&acc)[TM][TN], int m0, int n0,
+                                                  float* stage) {
+    constexpr int kPitch = BN + 4;
+    constexpr int kRuns = BN / 8;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const bool round_first = (p.flags & IDOLQ_FLAG_ROUND_BEFORE_BIAS) != 0;
+    __syncthreads();
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+        const int col = wn * WN + tn * 32 + (lane & 31);
+        const float bias = p.bias && n0 + col < p.n ? load_as_float(p.bias, p.bias_dt, n0 + col) : 0.0f;
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = wm * WM + tm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                float v = acc[tm][tn][r];
+                if (round_first) v = round_through(p.y_dt, v);
+                stage[row * kPitch + col] = v + bias;
+            }
+    }
+    __syncthreads();
+    for (int c = threadIdx.x; c < BM * kRuns; c += THREADS) {
+        const int row = c / kRuns, col = (c % kRuns) * 8;
+        const int grow = m0 + row, gcol = n0 + col;
+        if (grow >= p.m || gcol >= p.n) continue;
+        float v[8];
+        const float4 lo = *reinterpret_cast<const float4*>(stage + row * kPitch + col);
+        const float4 hi = *reinterpret_cast<const float4*>(stage + row * kPitch + col + 4);
+        v[0] = lo.x, v[1] = lo.y, v[2] = lo.z, v[3] = lo.w, v[4] = hi.x, v[5] = hi.y, v[6] = hi.z, v[7] = hi.w;
+        const int cnt = min(8, p.n - gcol);
+        if (cnt == 8 && p.y_vec) {
+            float r[8];
+            if (p.res) {
+                const char* rp = static_cast<const char*>(p.res) + ((int64_t)grow * p.ldr + gcol) * (p.res_dt == IDOLQ_F32 ? 4 : 2);
+                if (p.res_dt == IDOLQ_F32) {
+                    const float4 a = reinterpret_cast<const float4*>(rp)[0], b = reinterpret_cast<const float4*>(rp)[1];
+                    r[0] = a.x, r[1] = a.y, r[2] = a.z, r[3] = a.w, r[4] = b.x, r[5] = b.y, r[6] = b.z, r[7] = b.w;
+                } else {
+                    const uint4 u = *reinterpret_cast<const uint4*>(rp);
+                    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const uint16_t bits = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+                        r[e] = p.res_dt == IDOLQ_BF16 ? bf16_bits_to_float(bits) : half_bits_to_float(bits);
+                    }
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = apply_act(p.act, p.res ? v[e] + r[e] : v[e]);
+            char* yp = static_cast<char*>(p.y) + ((int64_t)grow * p.ldy + gcol) * (p.y_dt == IDOLQ_F32 ? 4 : 2);
+            if (p.y_dt == IDOLQ_F32) {
+                reinterpret_cast<float4*>(yp)[0] = make_float4(v[0], v[1], v[2], v[3]);
+                reinterpret_cast<float4*>(yp)[1] = make_float4(v[4], v[5], v[6], v[7]);
+            } else {
+                uint32_t w[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint16_t a = p.y_dt == IDOLQ_BF16 ? float_to_bf16_bits(v[2 * e]) : float_to_half_bits(v[2 * e]);
+                    const uint16_t b = p.y_dt == IDOLQ_BF16 ? float_to_bf16_bits(v[2 * e + 1]) : float_to_half_bits(v[2 * e + 1]);
+                    w[e] = (uint32_t)a | ((uint32_t)b << 16);
+                }
+                *reinterpret_cast<uint4*>(yp) = make_uint4(w[0], w[1], w[2], w[3]);
+            }
+        } else {
+            for (int e = 0; e < cnt; ++e) {
+                float x = v[e];
+                if (p.res) x += load_as_float(p.res, p.res_dt, (int64_t)grow * p.ldr + gcol + e);
+                store_from_float(p.y, p.y_dt, (int64_t)grow * p.ldy + gcol + e, apply_act(p.act, x));
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------------------------------------------ 16-bit MFMA kernel
-template <int BM, int BN, int XT, int MODE, bool W4>
-__global__ __launch_bounds__(kThreads) void q8_gemm_kernel(GemmParams p) {
+// Software pipeline with one barrier per stage. At the start of stage s: A[s%2] and B[s%2] hold stage s, raw[(s+1)%2]
+// holds stage s+1's weight bytes, one activation register set holds stage s+1 and one weight register set stage s+2.
+// During stage s each wave stores those registers (A[(s+1)%2], raw[s%2]), reloads them with activations s+3 and
+// weights s+4, converts raw[(s+1)%2] into B[(s+1)%2] and runs the MFMAs of stage s; every buffer it writes was last
+// read in stage s-1, before the barrier that ends it.
+template <int BM, int BN, int XT, int MODE, bool W4, int THREADS>
+__global__ __launch_bounds__(THREADS) void q8_gemm_kernel(GemmParams p) {
     typedef typename std::conditional<XT == XT_F16, _Float16, __bf16>::type T;
     typedef typename Mfma<T>::vec Vec;
     constexpr int NT = XT == XT_F32 ? 2 : 1;  // activation terms: bf16 high and low parts of fp32 input
-    constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
+    // waves in a (THREADS / 128) x 2 grid, each owning a WM x WN tile of 32 x 32 MFMA tiles
+    constexpr int WAVES_M = THREADS / 128;
+    constexpr int WM = BM / WAVES_M, WN = BN / 2, TM = WM / 32, TN = WN / 32;
 
-    __shared__ __attribute__((aligned(16))) uint16_t a_lds[NT][BM * kAPitch];
-    __shared__ __attribute__((aligned(16))) uint8_t code_lds[BN * kCodePitch];
-    __shared__ float scale_lds[BN * 2];
+    constexpr int kABytes = 2 * NT * BM * kAPitch * 2, kBBytes = 2 * BN * kAPitch * 2, kRawBytes = 2 * BN * 17 * 4;
+    constexpr int kScaleBytes = MODE == MODE_EXACT ? 2 * BN * 2 * 4 : 16;
+    constexpr int kLoopBytes = kABytes + kBBytes + kRawBytes + kScaleBytes;
+    constexpr int kStageBytes = BM * (BN + 4) * 4;
+    __shared__ __attribute__((aligned(16))) char smem[kLoopBytes > kStageBytes ? kLoopBytes : kStageBytes];
+    typedef uint16_t ATile[NT][BM * kAPitch];
+    typedef uint16_t BTile[BN * kAPitch];
+    typedef uint32_t RawTile[BN * 17];
+    typedef float ScaleTile[MODE == MODE_EXACT ? BN * 2 : 4];
+    ATile* a_lds = reinterpret_cast<ATile*>(smem);
+    BTile* b_lds = reinterpret_cast<BTile*>(smem + kABytes);
+    RawTile* raw_lds = reinterpret_cast<RawTile*>(smem + kABytes + kBBytes);
+    ScaleTile* bscale = reinterpret_cast<ScaleTile*>(smem + kABytes + kBBytes + kRawBytes);
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1;
@@ -302,67 +519,96 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_kernel(GemmParams p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    ActStage<BM, XT> as;
-    WeightStage<BN, W4> ws;
-    as.load(p, m0, 0);
-    ws.load(p, n0, 0, nblocks);
+    // Two register sets for the activation and weight loads, used alternately, so every load is issued two stages
+    // before its registers are stored to LDS: set (s + 1) % 2 of activations holds stage s + 1 at the start of
+    // stage s, set s % 2 of weights holds stage s + 2.
+    ActStage<BM, XT, THREADS> as0, as1;
+    RawStage<BN, W4, THREADS> ws0, ws1;
+    as0.init(p, m0);
+    as1.init(p, m0);
+    ws0.init(p, n0);
+    ws1.init(p, n0);
 
-    for (int s = 0; s < nsteps; ++s) {
-        __syncthreads();
-        as.store(a_lds[0], a_lds[NT - 1]);
-        ws.template store<kCodePitch>(code_lds, scale_lds);
-        __syncthreads();
-        if (s + 1 < nsteps) {
-            as.load(p, m0, (s + 1) * kKStep);
-            ws.load(p, n0, 2 * (s + 1), nblocks);
-        }
+    // prologue: A(0) and raw(0) into LDS, B(0) converted, raw(1) into LDS; then activations 1, 2 and weights 2, 3
+    // are in the registers
+    as0.load(p, 0);
+    ws0.load(p, 0, nblocks);
+    if (nsteps > 1) {
+        as1.load(p, kKStep);
+        ws1.load(p, 2, nblocks);
+    }
+    as0.store(a_lds[0][0], a_lds[0][NT - 1]);
+    ws0.store(raw_lds[0]);
+    if (nsteps > 2) {
+        as0.load(p, 2 * kKStep);
+        ws0.load(p, 4, nblocks);
+    }
+    __syncthreads();
+    convert_stage<T, BN, MODE, THREADS>(raw_lds[0], b_lds[0], bscale[0]);
+    if (nsteps > 1) ws1.store(raw_lds[1]);
+    if (nsteps > 3) ws1.load(p, 6, nblocks);
+    __syncthreads();
+
+    auto stage = [&](int s, auto& ra, auto& rw) {
+        // The body has no branches: past the last stage the prefetch indices are clamped and the stores and the
+        // conversion fill buffers that are never read again, so the whole stage is one scheduling region.
+        const int cur = s & 1, nxt = cur ^ 1;
+        ra.store(a_lds[nxt][0], a_lds[nxt][NT - 1]);
+        ra.load(p, min(s + 3, nsteps - 1) * kKStep);
+        rw.store(raw_lds[cur]);
+        rw.load(p, 2 * min(s + 4, nsteps - 1), nblocks);
+        convert_stage<T, BN, MODE, THREADS>(raw_lds[nxt], b_lds[nxt], bscale[nxt]);
+
+        const uint16_t* bc = b_lds[cur];
+        // Operands of both blocks of the stage are read before the first MFMA (the second block's reads complete
+        // under the first block's MFMAs).
+        Vec a[2][NT][TM][2], b[2][TN][2];
 #pragma unroll
-        for (int blk = 0; blk < 2; ++blk) {
-            Vec b[TN][2];
-            float d[TN];
+        for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
-            for (int tn = 0; tn < TN; ++tn) {
-                const int col = wn * WN + tn * 32 + (lane & 31);
-                d[tn] = scale_lds[col * 2 + blk];
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const uint2 raw = *reinterpret_cast<const uint2*>(code_lds + col * kCodePitch + blk * 32 + h * 16 +
-                                                                      (lane >> 5) * 8);
-                    b[tn][h] = codes_to_operand<T, MODE>(raw, d[tn]);
-                }
-            }
-#pragma unroll
-            for (int tm = 0; tm < TM; ++tm) {
-                const int row = wm * WM + tm * 32 + (lane & 31);
-                Vec a[NT][2];
+            for (int h = 0; h < 2; ++h) {
+                const int koff = blk * 32 + h * 16 + (lane >> 5) * 8;
 #pragma unroll
                 for (int t = 0; t < NT; ++t)
 #pragma unroll
-                    for (int h = 0; h < 2; ++h)
-                        a[t][h] = *reinterpret_cast<const Vec*>(a_lds[t] + row * kAPitch + blk * 32 + h * 16 +
-                                                                (lane >> 5) * 8);
+                    for (int tm = 0; tm < TM; ++tm)
+                        a[blk][t][tm][h] = *reinterpret_cast<const Vec*>(a_lds[cur][t] + (wm * WM + tm * 32 + (lane & 31)) * kAPitch + koff);
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn)
+                    b[blk][tn][h] = *reinterpret_cast<const Vec*>(bc + (wn * WN + tn * 32 + (lane & 31)) * kAPitch + koff);
+            }
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
                 for (int tn = 0; tn < TN; ++tn) {
                     if (MODE == MODE_DEQUANT) {
-                        acc[tm][tn] = Mfma<T>::run(a[0][0], b[tn][0], acc[tm][tn]);
-                        acc[tm][tn] = Mfma<T>::run(a[0][1], b[tn][1], acc[tm][tn]);
+                        acc[tm][tn] = Mfma<T>::run(a[blk][0][tm][0], b[blk][tn][0], acc[tm][tn]);
+                        acc[tm][tn] = Mfma<T>::run(a[blk][0][tm][1], b[blk][tn][1], acc[tm][tn]);
                     } else {
+                        const float d = bscale[cur][(wn * WN + tn * 32 + (lane & 31)) * 2 + blk];
                         f32x16 part;
 #pragma unroll
                         for (int r = 0; r < 16; ++r) part[r] = 0.0f;
 #pragma unroll
                         for (int t = 0; t < NT; ++t) {
-                            part = Mfma<T>::run(a[t][0], b[tn][0], part);
-                            part = Mfma<T>::run(a[t][1], b[tn][1], part);
+                            part = Mfma<T>::run(a[blk][t][tm][0], b[blk][tn][0], part);
+                            part = Mfma<T>::run(a[blk][t][tm][1], b[blk][tn][1], part);
                         }
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) acc[tm][tn][r] = fmaf(part[r], d[tn], acc[tm][tn][r]);
+                        for (int r = 0; r < 16; ++r) acc[tm][tn][r] = fmaf(part[r], d, acc[tm][tn][r]);
                     }
                 }
-            }
         }
+        __syncthreads();
+    };
+
+    for (int s = 0; s < nsteps; s += 2) {
+        stage(s, as1, ws0);
+        if (s + 1 < nsteps) stage(s + 1, as0, ws1);
     }
-    write_tile<TM, TN, WM, WN>(p, acc, m0, n0);
+    write_tile_staged<BM, BN, TM, TN, WM, WN, THREADS>(p, acc, m0, n0, reinterpret_cast<float*>(smem));
 }
 
 // ------------------------------------------------------------------------------------------------ int8 MFMA kernel
@@ -481,21 +727,69 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_int8_kernel(GemmParams p) {
 }
 
 // ------------------------------------------------------------------------------------------------ launch
-template <int BM, int BN>
-int launch_16bit(GemmParams p, int xt, int mode, bool w4, hipStream_t stream) {
+template <int BM, int BN, int THREADS>
+int launch_16bit_tile(GemmParams p, int xt, int mode, bool w4, hipStream_t stream) {
     p.tiles_m = (p.m + BM - 1) / BM;
     p.tiles_n = (p.n + BN - 1) / BN;
-    const dim3 grid(p.tiles_m * p.tiles_n), block(kThreads);
+    const dim3 grid(p.tiles_m * p.tiles_n), block(THREADS);
 #define IDOLQ_LAUNCH(XT, MODE, W4) \
-    hipLaunchKernelGGL((q8_gemm_kernel<BM, BN, XT, MODE, W4>), grid, block, 0, stream, p)
+    hipLaunchKernelGGL((q8_gemm_kernel<BM, BN, XT, MODE, W4, THREADS>), grid, block, 0, stream, p)
     if (xt == XT_BF16 && mode == MODE_DEQUANT) { if (w4) IDOLQ_LAUNCH(XT_BF16, MODE_DEQUANT, true); else IDOLQ_LAUNCH(XT_BF16, MODE_DEQUANT, false); }
     else if (xt == XT_BF16 && mode == MODE_EXACT) { if (w4) IDOLQ_LAUNCH(XT_BF16, MODE_EXACT, true); else IDOLQ_LAUNCH(XT_BF16, MODE_EXACT, false); }
     else if (xt == XT_F16 && mode == MODE_DEQUANT) { if (w4) IDOLQ_LAUNCH(XT_F16, MODE_DEQUANT, true); else IDOLQ_LAUNCH(XT_F16, MODE_DEQUANT, false); }
     else if (xt == XT_F16 && mode == MODE_EXACT) { if (w4) IDOLQ_LAUNCH(XT_F16, MODE_EXACT, true); else IDOLQ_LAUNCH(XT_F16, MODE_EXACT, false); }
-    else if (xt == XT_F32 && mode == MODE_EXACT) { if (w4) IDOLQ_LAUNCH(XT_F32, MODE_EXACT, true); else IDOLQ_LAUNCH(XT_F32, MODE_EXACT, false); }
     else return fail(IDOLQ_ENOSUPPORT, "this activation dtype does not support the requested GEMM mode");
 #undef IDOLQ_LAUNCH
     return check_launch("q8_gemm_kernel");
+}
+
+template <int BM, int BN>
+int launch_f32_tile(GemmParams p, bool w4, hipStream_t stream) {
+    p.tiles_m = (p.m + BM - 1) / BM;
+    p.tiles_n = (p.n + BN - 1) / BN;
+    const dim3 grid(p.tiles_m * p.tiles_n), block(kThreads);
+    if (w4)
+        hipLaunchKernelGGL((q8_gemm_kernel<BM, BN, XT_F32, MODE_EXACT, true, kThreads>), grid, block, 0, stream, p);
+    else
+        hipLaunchKernelGGL((q8_gemm_kernel<BM, BN, XT_F32, MODE_EXACT, false, kThreads>), grid, block, 0, stream, p);
+    return check_launch("q8_gemm_kernel");
+}
+
+// Tile choice: one workgroup per CU fits in LDS, so a launch runs in ceil(tiles / 256) rounds on the 256 CUs; pick
+// the tile with the smallest rounds * tile area / efficiency (the per-CU critical path). `eff` is the tile's measured
+// throughput relative to the 256 x 128 eight-wave tile on a large GEMM (4096 x 6144 x 1536).
+struct TileChoice {
+    int bm, bn;
+    float eff;
+};
+
+TileChoice choose_tile(int m, int n, const TileChoice* cands, int count) {
+    constexpr long kCUs = 256;
+    TileChoice best = cands[0];
+    float best_cost = -1.0f;
+    for (int i = 0; i < count; ++i) {
+        const long tiles = (long)((m + cands[i].bm - 1) / cands[i].bm) * ((n + cands[i].bn - 1) / cands[i].bn);
+        const float cost = (float)((tiles + kCUs - 1) / kCUs * cands[i].bm * cands[i].bn) / cands[i].eff;
+        if (best_cost < 0.0f || cost < best_cost) {
+            best = cands[i];
+            best_cost = cost;
+        }
+    }
+    return best;
+}
+
+int launch_16bit(GemmParams p, int xt, int mode, bool w4, hipStream_t stream) {
+    if (xt == XT_F32) {
+        static const TileChoice cands[] = {{128, 128, 1.0f}, {128, 64, 1.0f}};
+        const TileChoice t = choose_tile(p.m, p.n, cands, 2);
+        if (t.bn == 128) return launch_f32_tile<128, 128>(p, w4, stream);
+        return launch_f32_tile<128, 64>(p, w4, stream);
+    }
+    static const TileChoice cands[] = {{256, 128, 1.0f}, {128, 128, 0.5f}, {128, 64, 0.6f}};
+    const TileChoice t = choose_tile(p.m, p.n, cands, 3);
+    if (t.bm == 256) return launch_16bit_tile<256, 128, 512>(p, xt, mode, w4, stream);
+    if (t.bn == 128) return launch_16bit_tile<128, 128, kThreads>(p, xt, mode, w4, stream);
+    return launch_16bit_tile<128, 64, kThreads>(p, xt, mode, w4, stream);
 }
 
 template <int BM, int BN, bool DOTS>
@@ -542,6 +836,9 @@ extern "C" int idolq_q8_0_gemm(const void* x, int x_dtype, int64_t m, int64_t k,
     if (residual == y && residual && (residual_dtype != y_dtype || ldr != ldy))
         return fail(IDOLQ_EINVAL, "a residual that aliases y must have y's dtype and stride");
     if ((reinterpret_cast<uintptr_t>(w) & 1) != 0) return fail(IDOLQ_EINVAL, "Q8_0 weights must be 2-byte aligned");
+    // the kernels address activations and weights with 32-bit element / byte offsets
+    if (m * ldx >= (int64_t)UINT32_MAX || n * (k / kQ8Block) * kQ8Bytes >= (int64_t)UINT32_MAX)
+        return fail(IDOLQ_EINVAL, "x or the weight window exceeds 2^32 elements / bytes");
     if (mode == IDOLQ_MODE_AUTO) mode = x_dtype == IDOLQ_F32 ? IDOLQ_MODE_EXACT : IDOLQ_MODE_DEQUANT;
     if (mode < IDOLQ_MODE_DEQUANT || mode > IDOLQ_MODE_INT8) return fail(IDOLQ_EINVAL, "unknown GEMM mode");
     if (mode == IDOLQ_MODE_DEQUANT && x_dtype == IDOLQ_F32)
@@ -571,6 +868,9 @@ extern "C" int idolq_q8_0_gemm(const void* x, int x_dtype, int64_t m, int64_t k,
     const size_t esz = dtype_size(x_dtype);
     p.x_aligned = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && ((size_t)ldx * esz) % 16 == 0;
     const bool w4 = p.row_bytes % 4 == 0 && (reinterpret_cast<uintptr_t>(p.w) & 3) == 0;
+    const size_t ysz = dtype_size(y_dtype), rsz = residual ? dtype_size(residual_dtype) : 0;
+    p.y_vec = reinterpret_cast<uintptr_t>(y) % 16 == 0 && ((size_t)ldy * ysz) % 16 == 0 &&
+              (!residual || (reinterpret_cast<uintptr_t>(residual) % 16 == 0 && ((size_t)ldr * rsz) % 16 == 0));
 
     if (mode == IDOLQ_MODE_INT8) {
         const size_t need = idolq_q8_0_gemm_workspace(m, k, mode);
@@ -586,7 +886,7 @@ extern "C" int idolq_q8_0_gemm(const void* x, int x_dtype, int64_t m, int64_t k,
         return launch_int8<128, 128, false>(p, w4, s);
     }
     const int xt = x_dtype == IDOLQ_BF16 ? XT_BF16 : x_dtype == IDOLQ_F16 ? XT_F16 : XT_F32;
-    return launch_16bit<128, 128>(p, xt, mode == IDOLQ_MODE_DEQUANT ? MODE_DEQUANT : MODE_EXACT, w4, s);
+    return launch_16bit(p, xt, mode == IDOLQ_MODE_DEQUANT ? MODE_DEQUANT : MODE_EXACT, w4, s);
 }
 
 extern "C" int idolq_q8_0_block_dots(const int8_t* qa, int64_t m, int64_t k, const uint8_t* w, int64_t n_total,
