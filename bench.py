@@ -112,23 +112,82 @@ def run_gpu(args):
 
 
 def run_denoiser(args):
+    """One synthetic denoiser step: 24 layers, batch 2 (guidance pair) x 4096 tokens, context 2 x 1024 x 1280."""
     import torch
     import denoiser
 
     model = denoiser.SyntheticDenoiser.build(layers=args.denoiser_layers, seed=0)
-    x, ctx = model.inputs(seed=1)
+    x0, ctx = model.inputs(seed=1)
+    x = x0.clone()
     for _ in range(2):
+        x.copy_(x0)
         model.step(x, ctx)
     torch.cuda.synchronize()
     reps = 5
-    t0 = time.perf_counter()
+    times = []
     for _ in range(reps):
+        x.copy_(x0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
         model.step(x, ctx)
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / reps
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    ms = sorted(times)[reps // 2] * 1e3
     flop = model.flop_per_step()
-    return {"denoiser_step_ms": ms, "denoiser_tflops": flop / (ms * 1e-3) / 1e12,
-            "denoiser_layers": args.denoiser_layers}
+    out = {"denoiser_step_ms": round(ms, 3), "denoiser_tflops": round(flop / (ms * 1e-3) / 1e12, 2),
+           "denoiser_layers": args.denoiser_layers}
+    return out, model, ctx
+
+
+def run_cpu_denoiser_layer(model, ctx):
+    """The reference's CPU kernels (oracle/_ref: gemm_packed float kernel, norm_rows, attention, gelu_tanh) on one
+    full-size denoiser layer, all host cores; the step estimate is 24 x the layer."""
+    import numpy as np
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle as O
+
+    if not O.ref_available():
+        return {}
+    layer = model.layers[0]
+    B, S, Lc, H, hd = model.batch, model.seq, model.ctx_len, model.heads, model.head_dim
+    Dm = model.dim
+    w = {k: v.cpu().numpy() for k, v in layer.w.items()}
+    b = {k: v.cpu().numpy() for k, v in layer.b.items()}
+    blobs = {k: O.q8_0_to_panel(w[k], *layer.shape[k]) for k in w}
+    gen = np.random.default_rng(0)
+    x = gen.standard_normal((B * S, Dm), dtype=np.float32)
+    c = ctx.float().cpu().numpy()
+    shift, scale = model.shift.cpu().numpy(), model.scale.cpu().numpy()
+
+    def lin(name, a, residual=None):
+        n, k = layer.shape[name]
+        return O.ref_gemm_panel(a, blobs[name], b[name], n, k, residual=residual, mode=0)
+
+    def one_layer(x):
+        h = np.concatenate([O.ref_norm_rows(x[i * S:(i + 1) * S], 1e-6, shift=shift[i], scale=scale[i]) for i in range(B)])
+        qkv = lin("qkv", h)
+        # q, k and v are column ranges of the [S, 3D] projection rows: flat slices at offsets 0, D and 2D
+        att = np.concatenate([O.ref_attention(qkv[i * S:(i + 1) * S].reshape(-1), qkv[i * S:(i + 1) * S].reshape(-1)[Dm:],
+                                              qkv[i * S:(i + 1) * S].reshape(-1)[2 * Dm:], S, S, 3 * Dm, 3 * Dm, H, hd)
+                              for i in range(B)])
+        x = lin("out", att, residual=x)
+        q = lin("cq", O.ref_norm_rows(x, 1e-6))
+        kv = lin("ckv", c)
+        att = np.concatenate([O.ref_attention(q[i * S:(i + 1) * S], kv[i * Lc:(i + 1) * Lc].reshape(-1),
+                                              kv[i * Lc:(i + 1) * Lc].reshape(-1)[Dm:], S, Lc, Dm, 2 * Dm, H, hd)
+                              for i in range(B)])
+        x = lin("cout", att, residual=x)
+        f = O.ref_gelu_tanh(lin("up", O.ref_norm_rows(x, 1e-6)))
+        return lin("down", f, residual=x)
+
+    t0 = time.perf_counter()
+    one_layer(x)
+    t = time.perf_counter() - t0
+    cores = int(os.environ.get("OMP_NUM_THREADS", 0)) or os.cpu_count()
+    return {"denoiser_cpu_layer_ms": round(t * 1e3, 1), "denoiser_cpu_step_ms_est": round(24 * t * 1e3, 1),
+            "denoiser_cpu_cores": cores,
+            "denoiser_cpu_note": "reference kernels.cpp float kernel + attention + norm_rows + gelu_tanh on one "
+                                 "full-size layer (batch 2 x 4096 tokens), step = 24 x layer"}
 
 
 def run_cpu_baseline(args, inputs):
@@ -194,13 +253,17 @@ def main():
         "roofline": gpu["roofline"],
         "pct_int8_peak": round(gpu["pct_int8_peak"], 4),
     }
+    model = ctx = None
     if not args.no_denoiser:
-        try:
-            result.update(run_denoiser(args))
-        except ImportError:
-            result["denoiser_step_ms"] = None
+        dn, model, ctx = run_denoiser(args)
+        result.update(dn)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = run_cpu_baseline(args, inputs)
+        if model is not None:
+            cpu = run_cpu_denoiser_layer(model, ctx)
+            result.update(cpu)
+            if cpu:
+                result["denoiser_speedup_vs_cpu"] = round(cpu["denoiser_cpu_step_ms_est"] / result["denoiser_step_ms"], 1)
     print(json.dumps(result), flush=True)
 
 

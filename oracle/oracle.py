@@ -323,6 +323,8 @@ def ref_norm_rows(x, eps, gamma=None, beta=None, shift=None, scale=None):
 def ref_attention(q, k, v, lq, lk, ldq, ldkv, heads, head_dim):
     q, k, v = _f32(q), _f32(k), _f32(v)
     dim = heads * head_dim
+    if q.size < (lq - 1) * ldq + dim or k.size < (lk - 1) * ldkv + dim or v.size < (lk - 1) * ldkv + dim:
+        raise ValueError("attention buffers are smaller than their rows and strides")
     out = np.empty((lq, dim), np.float32)
     ref_lib().ref_attention(_ptr(q), lq, ldq, _ptr(k), _ptr(v), lk, ldkv, heads, head_dim, out, dim)
     return out
