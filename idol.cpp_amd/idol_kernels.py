@@ -41,7 +41,7 @@ def quant_panel_bytes(in_, bits, group):
 
 
 def set_quant_kernel(mode):
-    """src/kernels.hpp:62-64. -1: IDOL_QUANT_KERNEL decides ("float" forces the float kernel), 0: float, 1: int8."""
+    """src/kernels.hpp:64-68. -1: IDOL_QUANT_KERNEL decides ("float" forces the float kernel), 0: float, 1: int8."""
     global _quant_kernel
     _quant_kernel = int(mode)
 
@@ -116,7 +116,7 @@ def dequantize_linear(w):
 
 
 def gemm_packed(a, m, w, n_offset, n, residual, gelu, c):
-    """c[m x n] = a[m x in] * W^T + bias for output columns [n_offset, n_offset + n) (src/kernels.hpp:70-74).
+    """c[m x n] = a[m x in] * W^T + bias for output columns [n_offset, n_offset + n) (src/kernels.hpp:73-76).
 
     a is [m, in] fp32 (rows unit-stride); c and residual are [m, n] (residual may alias c); the residual is added
     before the optional erf-GELU."""
@@ -142,7 +142,7 @@ def norm_rows(x, y, rows, dim, eps, gamma=None, beta=None, shift=None, scale=Non
 
 
 def attention(q, lq, ldq, k, v, lk, ldkv, heads, head_dim, out, dim):
-    """Scaled dot-product attention over projected rows (src/kernels.hpp:84-86). q, k, v and out are flat GPU
+    """Scaled dot-product attention over projected rows (src/kernels.hpp:81-84). q, k, v and out are flat GPU
     tensors (pointer offsets as views); q has lq rows of stride ldq, k and v lk rows of stride ldkv, out lq rows of
     stride dim."""
     return L.attention(q, k, v, 1, lq, lk, heads, head_dim, ldq, ldkv, 0, 0, out, dim, 0)

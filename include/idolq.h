@@ -64,7 +64,7 @@ int64_t idolq_q8_0_bytes(int64_t n, int64_t k);
  *   act      IDOLQ_ACT_*, applied after bias and residual
  *   y        [m x n] in y_dtype, row stride ldy
  *   workspace / workspace_bytes  scratch for IDOLQ_MODE_INT8 (idolq_q8_0_gemm_workspace bytes), else may be NULL
- * Replaces src/kernels.hpp:70-74 gemm_packed (fp32 x, residual before GELU, column window n_offset / n) and
+ * Replaces src/kernels.hpp:73-76 gemm_packed (fp32 x, residual before GELU, column window n_offset / n) and
  * tools/idol_triton.py:94-126 fused_linear (bf16/fp16 x, bias after rounding: IDOLQ_FLAG_ROUND_BEFORE_BIAS). */
 int idolq_q8_0_gemm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* w, int64_t n_total,
                     int64_t n_offset, int64_t n, const void* bias, int bias_dtype, const void* residual,
@@ -111,7 +111,7 @@ int idolq_layernorm(const void* x, int x_dtype, int64_t rows, int64_t dim, int64
  *   out  [batch][lq rows of stride ldo], batch stride o_bs
  * q, k, v share `dtype`; out has out_dtype. bf16/fp16 inputs use MFMA (QK^T in the input type, fp32 online softmax,
  * P and V in fp16 for P*V); fp32 inputs and head_dim other than 64 use an fp32 kernel.
- * Replaces src/kernels.hpp:84-86 attention (batch 1, out stride dim). */
+ * Replaces src/kernels.hpp:81-84 attention (batch 1, out stride dim). */
 int idolq_attention(const void* q, const void* k, const void* v, int dtype, int64_t batch, int64_t lq, int64_t lk,
                     int64_t heads, int64_t head_dim, int64_t ldq, int64_t ldkv, int64_t q_bs, int64_t kv_bs, void* out,
                     int out_dtype, int64_t ldo, int64_t o_bs, void* stream);
