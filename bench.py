@@ -17,6 +17,7 @@ Also reported, in the same JSON line:
 import argparse
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -28,6 +29,10 @@ METRIC = "Q8_0 GEMM TFLOP/s (% int8 MFMA peak) + denoiser-step ms at seq 4096, 1
 PEAK_TFLOPS = {"bf16": 2500.0, "fp16": 2500.0, "int8": 5000.0}
 HBM_GBS = 8000.0
 M, D, H = 4096, 1536, 6144
+# Minimum HBM bytes of one launch: Q8_0 weights (34 B per 32 weights) + bf16 activations in + out (+ bias fp32,
+# + residual for the down projection)
+ALG_BYTES_UP = H * D // 32 * 34 + M * D * 2 + M * H * 2 + H * 4
+ALG_BYTES_DOWN = D * H // 32 * 34 + M * H * 2 + M * D * 2 * 2 + D * 4
 
 
 def parse():
@@ -42,6 +47,9 @@ def parse():
     p.add_argument("--no-denoiser", action="store_true")
     p.add_argument("--denoiser-layers", type=int, default=24)
     p.add_argument("--cpu-rows", type=int, default=1024, help="rows of the MLP block the CPU baseline runs")
+    p.add_argument("--traffic-probe", action="store_true",
+                   help="launch only the calibration copy (512 MiB bf16) and the two GEMMs, 3 times each, untimed: the "
+                        "program rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs to measure HBM bytes per launch")
     return p.parse_args()
 
 
@@ -53,6 +61,44 @@ def mlp_inputs(torch, L, seed=0):
     b_up = torch.randn(H, device="cuda", generator=gen) * 0.01
     b_down = torch.randn(D, device="cuda", generator=gen) * 0.01
     return x, w_up, w_down, b_up, b_down
+
+
+TRAFFIC_FILE = ROOT / "profiles" / "q8_gemm_mlp_block_traffic.md"
+COPY_ROWS, COPY_COLS = 16384, 16384  # bf16: 512 MiB read + 512 MiB written, twice the 256 MB Infinity Cache
+
+
+def run_traffic_probe(args):
+    import torch
+    import idolq_lib as L
+
+    mode = {"dequant": L.MODE_DEQUANT, "exact": L.MODE_EXACT, "int8": L.MODE_INT8}[args.mode]
+    x, w_up, w_down, b_up, b_down = mlp_inputs(torch, L)
+    h = torch.empty((M, H), device="cuda", dtype=torch.bfloat16)
+    y = torch.empty((M, D), device="cuda", dtype=torch.bfloat16)
+    ws = torch.empty(max(L.load().idolq_q8_0_gemm_workspace(M, H, mode), 16), device="cuda", dtype=torch.uint8)
+    src = torch.empty((COPY_ROWS, COPY_COLS), device="cuda", dtype=torch.bfloat16).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        L.copy2d(src, dst)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        L.gemm(x, w_up, H, bias=b_up, act=L.ACT_GELU_TANH, mode=mode, out=h, workspace=ws)
+        L.gemm(h, w_down, D, bias=b_down, residual=x, mode=mode, out=y, workspace=ws)
+    torch.cuda.synchronize()
+    print(json.dumps({"traffic_probe": "done", "copy_bytes": COPY_ROWS * COPY_COLS * 2}), flush=True)
+
+
+def measured_traffic():
+    """HBM bytes per GEMM launch from the committed --pmc summary (lines 'traffic_bytes up=<B> down=<B>'), or None."""
+    try:
+        text = TRAFFIC_FILE.read_text()
+    except OSError:
+        return None
+    m = re.search(r"traffic_bytes up=(\d+) down=(\d+)", text)
+    if not m:
+        return None
+    up, down = int(m.group(1)), int(m.group(2))
+    return {"up": up, "down": down, "mean": (up + down) / 2}
 
 
 def run_gpu(args):
@@ -95,13 +141,16 @@ def run_gpu(args):
     value = 2 * flop_gemm / (ms_per_step * 1e-3) / 1e12
     arith = {"dequant": "bf16", "exact": "bf16", "int8": "int8"}[args.mode]
     gemm_ms = (up_ms + down_ms) / 2
+    traffic = measured_traffic() if args.mode == "dequant" else None
     achieved = flop_gemm / (gemm_ms * 1e-3) / 1e12
     out = {
         "value": value,
         "ms_per_step": ms_per_step,
         "dtype": arith,
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_TFLOPS[arith], "unit": "TFLOP/s",
-                     "frac": achieved / PEAK_TFLOPS[arith], "traffic": None,
+                     "frac": achieved / PEAK_TFLOPS[arith], "traffic": traffic["mean"] if traffic else None,
+                     "traffic_per_launch": traffic,
+                     "algorithmic_bytes": {"up": ALG_BYTES_UP, "down": ALG_BYTES_DOWN},
                      "kernel": "q8_gemm_kernel" if args.mode != "int8" else "q8_gemm_int8_kernel",
                      "launch_ms": {"up": up_ms, "down": down_ms},
                      "flop_per_launch": flop_gemm},
@@ -233,6 +282,9 @@ def main():
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py runs on exactly one GPU: this build has no multi-GPU path (--gpus must be 1)", file=sys.stderr)
         sys.exit(2)
+    if args.traffic_probe:
+        run_traffic_probe(args)
+        return
     gpu, inputs = run_gpu(args)
     result = {
         "metric": METRIC,

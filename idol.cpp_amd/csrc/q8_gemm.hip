@@ -15,7 +15,7 @@
 // MFMA operand layout (32 x 32 tiles): lane l supplies row (or column) l % 32 and the 8 (bf16/fp16, 16-deep
 // instruction) or 16 (int8, 32-deep) consecutive k starting at (l / 32) * 8 (resp. 16); accumulator element r of
 // lane l is row 8 * (r / 4) + 4 * (l / 32) + r % 4, column l % 32.
-#include "common.h"
+#include "q8_gemm.h"
 
 #include <type_traits>
 
@@ -26,51 +26,6 @@ constexpr int kThreads = 256;
 constexpr int kKStep = 64;                // depth per stage: two Q8_0 blocks
 constexpr int kAPitch = kKStep + 8;       // 16-bit elements per activation row in LDS (144 bytes)
 constexpr int kCodePitch8 = kKStep + 16;  // bytes per row of int8 operands for 16-byte reads (80)
-
-enum { XT_BF16 = 0, XT_F16 = 1, XT_F32 = 2 };
-enum { MODE_DEQUANT = 1, MODE_EXACT = 2 };
-
-struct GemmParams {
-    const void* x;
-    int64_t ldx;
-    const uint8_t* w;  // row 0 of the column window
-    int64_t row_bytes;
-    int m, n, k;
-    const void* bias;  // entry 0 of the column window
-    int bias_dt;
-    const void* res;
-    int res_dt;
-    int64_t ldr;
-    void* y;
-    int y_dt;
-    int64_t ldy;
-    int act, flags;
-    int tiles_m, tiles_n;
-    int x_aligned;  // x rows are 16-byte aligned
-    int y_vec;      // y (and the residual, when given) rows and base are 16-byte aligned: vector epilogue stores
-    // INT8 mode
-    const int8_t* qa;
-    const float* sa;
-    int32_t* dots;
-};
-
-// ------------------------------------------------------------------------------------------------ tile order
-// Workgroup b runs on XCD b % 8. Consecutive logical tiles are given to the same XCD, and logical tiles walk
-// groups of 8 row-tiles column by column, so workgroups resident together on one XCD share weight rows and
-// activation rows in that XCD's L2.
-__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, int& tn) {
-    const int total = tiles_m * tiles_n;
-    int b = blockIdx.x;
-    if (total % 8 == 0) b = (b % 8) * (total / 8) + b / 8;
-    constexpr int G = 8;
-    const int per_group = G * tiles_n;
-    const int group = b / per_group;
-    const int first = group * G;
-    const int gm = min(tiles_m - first, G);
-    const int in_group = b - group * per_group;
-    tm = first + in_group % gm;
-    tn = in_group / gm;
-}
 
 // ------------------------------------------------------------------------------------------------ weight staging
 // Flat loader for the 68 bytes (two blocks) of each of BN weight rows per stage.
@@ -156,6 +111,7 @@ struct ActStage {
     static_assert(BM % kRowsPerPass == 0, "tile size");
     uint32_t off[kPer];  // element offset of the unit's row start + column unit, ~0u when the row is outside m
     uint4 v[kPer];
+    bool ok[kPer];  // the unit holds x (else it is stored as zeros)
 
     __device__ __forceinline__ void init(const GemmParams& p, int m0) {
         const int cu = threadIdx.x % kUnitsPerRow, r0 = threadIdx.x / kUnitsPerRow;
@@ -166,24 +122,24 @@ struct ActStage {
         }
     }
 
-    // Invalid units (rows outside m, depth beyond k) read the first element of x and are zeroed by a select, so the
-    // loads need no branches.
+    // Invalid units (rows outside m, depth beyond k) read the first element of x and are zeroed when stored (not
+    // when loaded, which would make the load's consumer wait for it), so the loads need no branches.
     __device__ __forceinline__ void load(const GemmParams& p, int k0) {
         const int kk = k0 + (threadIdx.x % kUnitsPerRow) * kElems;
         const bool kin = kk < p.k;
         if (p.x_aligned) {
 #pragma unroll
             for (int i = 0; i < kPer; ++i) {
-                const bool ok = off[i] != ~0u && kin;
-                const char* src = static_cast<const char*>(p.x) + (ok ? ((size_t)off[i] + k0) * kEsz : 0);
-                const uint4 t = *reinterpret_cast<const uint4*>(src);
-                v[i] = ok ? t : make_uint4(0, 0, 0, 0);
+                ok[i] = off[i] != ~0u && kin;
+                const char* src = static_cast<const char*>(p.x) + (ok[i] ? ((size_t)off[i] + k0) * kEsz : 0);
+                v[i] = *reinterpret_cast<const uint4*>(src);
             }
             return;
         }
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
             v[i] = make_uint4(0, 0, 0, 0);
+            ok[i] = true;
             if (off[i] != ~0u && kin) {
                 const char* src = static_cast<const char*>(p.x) + ((size_t)off[i] + k0) * kEsz;
                 {
@@ -208,11 +164,12 @@ struct ActStage {
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
             const int off_lds = (r0 + i * kRowsPerPass) * kAPitch + cu * kElems;
+            const uint4 vi = ok[i] ? v[i] : make_uint4(0, 0, 0, 0);
             if (XT != XT_F32) {
-                *reinterpret_cast<uint4*>(hi + off_lds) = v[i];
+                *reinterpret_cast<uint4*>(hi + off_lds) = vi;
             } else {
-                const float f[4] = {__builtin_bit_cast(float, v[i].x), __builtin_bit_cast(float, v[i].y),
-                                    __builtin_bit_cast(float, v[i].z), __builtin_bit_cast(float, v[i].w)};
+                const float f[4] = {__builtin_bit_cast(float, vi.x), __builtin_bit_cast(float, vi.y),
+                                    __builtin_bit_cast(float, vi.z), __builtin_bit_cast(float, vi.w)};
                 uint32_t h[2], l[2];
 #pragma unroll
                 for (int e = 0; e < 2; ++e) {
@@ -241,6 +198,7 @@ struct RawStage {
     uint32_t off[kPer];  // byte offset of the unit within the window (row * row_bytes + part * size), ~0u if unused
     bool second[kPer];   // the unit belongs to the second block of the stage
     uint32_t v[kPer];
+    bool ok[kPer];  // the unit holds weight bytes (else it is stored as zero)
 
     __device__ __forceinline__ void init(const GemmParams& p, int n0) {
 #pragma unroll
@@ -253,15 +211,15 @@ struct RawStage {
         }
     }
 
-    // Units outside the window (or in a missing second block) read the window's first bytes and are zeroed.
+    // Units outside the window (or in a missing second block) read the window's first bytes and are zeroed when
+    // stored.
     __device__ __forceinline__ void load(const GemmParams& p, int blk0, int nblocks) {
         const bool has_second = blk0 + 1 < nblocks;
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
-            const bool ok = off[i] != ~0u && (has_second || !second[i]);
-            const uint8_t* src = p.w + (ok ? off[i] + (size_t)blk0 * kQ8Bytes : 0);
-            const uint32_t t = W4 ? *reinterpret_cast<const uint32_t*>(src) : (uint32_t) * reinterpret_cast<const uint16_t*>(src);
-            v[i] = ok ? t : 0u;
+            ok[i] = off[i] != ~0u && (has_second || !second[i]);
+            const uint8_t* src = p.w + (ok[i] ? off[i] + (size_t)blk0 * kQ8Bytes : 0);
+            v[i] = W4 ? *reinterpret_cast<const uint32_t*>(src) : (uint32_t) * reinterpret_cast<const uint16_t*>(src);
         }
     }
 
@@ -270,10 +228,11 @@ struct RawStage {
         for (int i = 0; i < kPer; ++i) {
             const int u = threadIdx.x + i * THREADS;
             if (u < kUnits) {
+                const uint32_t vi = ok[i] ? v[i] : 0u;
                 if (W4)
-                    raw[u] = v[i];
+                    raw[u] = vi;
                 else
-                    reinterpret_cast<uint16_t*>(raw)[u] = (uint16_t)v[i];
+                    reinterpret_cast<uint16_t*>(raw)[u] = (uint16_t)vi;
             }
         }
     }
@@ -787,6 +746,7 @@ int launch_16bit(GemmParams p, int xt, int mode, bool w4, hipStream_t stream) {
     }
     static const TileChoice cands[] = {{256, 128, 1.0f}, {128, 128, 0.5f}, {128, 64, 0.6f}};
     const TileChoice t = choose_tile(p.m, p.n, cands, 3);
+    if (t.bm == 256 && pipe_eligible(p, xt, mode)) return launch_pipe(p, xt, stream);
     if (t.bm == 256) return launch_16bit_tile<256, 128, 512>(p, xt, mode, w4, stream);
     if (t.bn == 128) return launch_16bit_tile<128, 128, kThreads>(p, xt, mode, w4, stream);
     return launch_16bit_tile<128, 64, kThreads>(p, xt, mode, w4, stream);
