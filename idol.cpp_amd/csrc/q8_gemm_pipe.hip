@@ -234,8 +234,10 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
         lds_dma4(base, w_off[4], lds0 + w_dst4 + (w_dst4 == kJunk ? 0 : (s % 3) * kRawBuf));
     };
 
-    // ---- weight conversion: thread -> row tid / 4, chunk q = tid % 4 of each block (8 codes per block)
-    const int cv_row = tid >> 2, cv_q = tid & 3;
+    // ---- weight conversion: thread -> row tid % 128, chunk q = tid / 128 of each block (8 codes per block).
+    // Consecutive lanes take consecutive rows, so each 4-byte read (row stride 17 dwords, odd) hits 64 distinct banks
+    // and each 16-byte write (row stride 144 bytes) 16 distinct 4-bank groups per cycle.
+    const int cv_row = tid & (kPipeBN - 1), cv_q = tid >> 7;
     struct RawIn {
         uint32_t w0, w8, a0, a1, a2, b0, b1;
     };
@@ -326,17 +328,24 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
     // with the LDS reads and the conversion arithmetic issued between them (the matrix core runs an MFMA while the
     // wave issues the following independent instructions).
     auto stage_steady = [&](int s) {
-        issue_a(s + 3);
-        issue_w(s + 4);
         const RawIn raw = convert_load(s + 2);
         __builtin_amdgcn_sched_barrier(0);
-        // four segments, one per operand group: its 4 MFMAs, the reads of stage s + 1's operands of the group and a
-        // quarter of the conversion (4 codes)
+        // four segments, one per operand group: a quarter of the global loads (one activation load, one or two
+        // weight loads), the group's 4 MFMAs, the reads of stage s + 1's operands of the group and a quarter of the
+        // conversion (4 codes). Spreading the loads over the stage keeps the vector-memory queue from filling up and
+        // stalling the wave in front of its MFMAs.
         const float d0 = half_bits_to_float((uint16_t)(raw.w0 & 0xffff));
         const float d1 = half_bits_to_float((uint16_t)(raw.w8 >> 16));
         char* bdst = smem + kBBase + (s & 1) * kBBuf + cv_row * kBPitch + cv_q * 16;
+        const char* abase = xg + (size_t)(s + 3) * 128;
+        const uint32_t adst = lds0 + ((s + 3) % 3) * kABuf + wave * 1024;
+        const char* wbase = wg + (size_t)(s + 4) * 68;
+        const int wslot = (s + 4) % 3;
+        const uint32_t wdst = lds0 + kRawBase + wslot * kRawBuf + wave * 256;
         uint2 q0, q1, q2, q3;
 #define IDOLQ_SEGMENT(G, WORK)                                     \
+        lds_dma16(abase, a_off[G], adst + G * 8192);               \
+        lds_dma4(wbase, w_off[G], wdst + G * 2048);                \
         mfma_group(G);                                             \
         read_group(s + 1, G);                                      \
         WORK;                                                      \
@@ -361,6 +370,7 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
         IDOLQ_SEGMENT(3, q3 = dequant4<T>(raw.b1, d1);
                          *reinterpret_cast<uint4*>(bdst + 64) = make_uint4(q2.x, q2.y, q3.x, q3.y));
 #undef IDOLQ_SEGMENT
+        lds_dma4(wbase, w_off[4], lds0 + w_dst4 + (w_dst4 == kJunk ? 0 : wslot * kRawBuf));
         // activations s + 2 and weight bytes s + 3 (issued in stage s - 1) have landed once at most the 9 loads
         // issued in this stage remain outstanding
         wait_vm<9>();
