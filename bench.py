@@ -9,7 +9,9 @@ per step / measured time, in TFLOP/s.
 
 Also reported, in the same JSON line:
   roofline       the GEMM kernel's average launch time from HIP events on its stream over the timed steps;
-                 achieved = 2 * M * N * K / launch time against the MFMA peak of the arithmetic it runs
+                 achieved = 2 * M * N * K / launch time against the MFMA peak of the arithmetic it runs; traffic =
+                 HBM bytes per launch from the committed rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE summary of the
+                 --traffic-probe run (profiles/q8_gemm_mlp_block_traffic.md), scaled by a copy kernel of known size
   pct_int8_peak  value as a fraction of the gfx950 dense int8 MFMA peak (5.0 POP/s), as the metric asks
   denoiser_step_ms  one full synthetic denoiser step (24 layers, batch 2 x 4096 tokens), unless --no-denoiser
   cpu_baseline   the reference's own CPU kernels (oracle/_ref, float kernel, all host cores) on the same MLP block
@@ -63,6 +65,31 @@ def mlp_inputs(torch, L, seed=0):
     return x, w_up, w_down, b_up, b_down
 
 
+class MlpBlock:
+    """The MLP block on preallocated buffers. DEQUANT reads the weights in the tiled Q8_0 layout (the same blocks,
+    reordered once at load time); INT8 and EXACT read the GGUF row-major blocks (INT8 with its workspace)."""
+
+    def __init__(self, torch, L, mode, inputs):
+        self.L, self.mode = L, mode
+        self.x, w_up, w_down, self.b_up, self.b_down = inputs
+        self.tiled = mode == L.MODE_DEQUANT
+        self.w_up = L.tile_q8_0(w_up, H, D) if self.tiled else w_up
+        self.w_down = L.tile_q8_0(w_down, D, H) if self.tiled else w_down
+        self.h = torch.empty((M, H), device="cuda", dtype=torch.bfloat16)
+        self.y = torch.empty((M, D), device="cuda", dtype=torch.bfloat16)
+        self.ws = None
+        if mode == L.MODE_INT8:
+            self.ws = torch.empty(L.load().idolq_q8_0_gemm_workspace(M, H, mode), device="cuda", dtype=torch.uint8)
+
+    def up(self):
+        self.L.gemm(self.x, self.w_up, H, bias=self.b_up, act=self.L.ACT_GELU_TANH, mode=self.mode, out=self.h,
+                    workspace=self.ws, tiled=self.tiled)
+
+    def down(self):
+        self.L.gemm(self.h, self.w_down, D, bias=self.b_down, residual=self.x, mode=self.mode, out=self.y,
+                    workspace=self.ws, tiled=self.tiled)
+
+
 TRAFFIC_FILE = ROOT / "profiles" / "q8_gemm_mlp_block_traffic.md"
 COPY_ROWS, COPY_COLS = 16384, 16384  # bf16: 512 MiB read + 512 MiB written, twice the 256 MB Infinity Cache
 
@@ -72,18 +99,15 @@ def run_traffic_probe(args):
     import idolq_lib as L
 
     mode = {"dequant": L.MODE_DEQUANT, "exact": L.MODE_EXACT, "int8": L.MODE_INT8}[args.mode]
-    x, w_up, w_down, b_up, b_down = mlp_inputs(torch, L)
-    h = torch.empty((M, H), device="cuda", dtype=torch.bfloat16)
-    y = torch.empty((M, D), device="cuda", dtype=torch.bfloat16)
-    ws = torch.empty(max(L.load().idolq_q8_0_gemm_workspace(M, H, mode), 16), device="cuda", dtype=torch.uint8)
+    blk = MlpBlock(torch, L, mode, mlp_inputs(torch, L))
     src = torch.empty((COPY_ROWS, COPY_COLS), device="cuda", dtype=torch.bfloat16).fill_(1.0)
     dst = torch.empty_like(src)
     for _ in range(3):
         L.copy2d(src, dst)
     torch.cuda.synchronize()
     for _ in range(3):
-        L.gemm(x, w_up, H, bias=b_up, act=L.ACT_GELU_TANH, mode=mode, out=h, workspace=ws)
-        L.gemm(h, w_down, D, bias=b_down, residual=x, mode=mode, out=y, workspace=ws)
+        blk.up()
+        blk.down()
     torch.cuda.synchronize()
     print(json.dumps({"traffic_probe": "done", "copy_bytes": COPY_ROWS * COPY_COLS * 2}), flush=True)
 
@@ -106,18 +130,16 @@ def run_gpu(args):
     import idolq_lib as L
 
     mode = {"dequant": L.MODE_DEQUANT, "exact": L.MODE_EXACT, "int8": L.MODE_INT8}[args.mode]
-    x, w_up, w_down, b_up, b_down = mlp_inputs(torch, L)
-    h = torch.empty((M, H), device="cuda", dtype=torch.bfloat16)
-    y = torch.empty((M, D), device="cuda", dtype=torch.bfloat16)
-    ws = torch.empty(max(L.load().idolq_q8_0_gemm_workspace(M, H, mode), 16), device="cuda", dtype=torch.uint8)
+    inputs = mlp_inputs(torch, L)
+    blk = MlpBlock(torch, L, mode, inputs)
 
     def step(events=None):
         if events is not None:
             events[0].record()
-        L.gemm(x, w_up, H, bias=b_up, act=L.ACT_GELU_TANH, mode=mode, out=h, workspace=ws)
+        blk.up()
         if events is not None:
             events[1].record()
-        L.gemm(h, w_down, D, bias=b_down, residual=x, mode=mode, out=y, workspace=ws)
+        blk.down()
         if events is not None:
             events[2].record()
 
@@ -151,13 +173,14 @@ def run_gpu(args):
                      "frac": achieved / PEAK_TFLOPS[arith], "traffic": traffic["mean"] if traffic else None,
                      "traffic_per_launch": traffic,
                      "algorithmic_bytes": {"up": ALG_BYTES_UP, "down": ALG_BYTES_DOWN},
-                     "kernel": "q8_gemm_kernel" if args.mode != "int8" else "q8_gemm_int8_kernel",
+                     "kernel": "q8_gemm_pipe_kernel" if args.mode == "dequant" else
+                               "q8_gemm_kernel" if args.mode == "exact" else "q8_gemm_int8_kernel",
                      "launch_ms": {"up": up_ms, "down": down_ms},
                      "flop_per_launch": flop_gemm},
         "pct_int8_peak": value / PEAK_TFLOPS["int8"],
     }
-    del h, y, ws
-    return out, (x, w_up, w_down, b_up, b_down)
+    del blk
+    return out, inputs
 
 
 def run_denoiser(args):

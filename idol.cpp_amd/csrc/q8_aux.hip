@@ -192,6 +192,38 @@ extern "C" int idolq_q8_0_dequant(const uint8_t* w, int64_t n, int64_t k, void* 
     return check_launch("q8_dequant_kernel");
 }
 
+// One dword of the tiled layout per thread: dword u of chunk (t, s) is dword u % 17 of stage s of row t * 128 + u / 17
+// (zero past the last row). Rows are 4-byte aligned since k % 64 == 0.
+__global__ __launch_bounds__(256) void q8_tile_kernel(const uint32_t* __restrict__ w, int64_t n, int64_t row_dwords,
+                                                      int stages, int64_t total, uint32_t* __restrict__ out) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t chunk = i / 2176;
+        const int u = (int)(i - chunk * 2176);
+        const int64_t t = chunk / stages;
+        const int s = (int)(chunk - t * stages);
+        const int64_t row = t * 128 + u / 17;
+        out[i] = row < n ? w[row * row_dwords + (int64_t)s * 17 + u % 17] : 0u;
+    }
+}
+
+extern "C" int64_t idolq_q8_0_tiled_bytes(int64_t n, int64_t k) {
+    if (n < 0 || k <= 0 || k % 64) return 0;
+    return (n + 127) / 128 * (k / 64) * 8704;
+}
+
+extern "C" int idolq_q8_0_tile(const uint8_t* w, int64_t n, int64_t k, uint8_t* out, void* stream) {
+    if (n < 0 || k <= 0 || k % 64) return fail(IDOLQ_EINVAL, "tiled Q8_0 needs n >= 0 and k a positive multiple of 64");
+    if (n == 0) return IDOLQ_OK;
+    if (!w || !out) return fail(IDOLQ_EINVAL, "w and out must be non-null");
+    if ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(out)) & 3)
+        return fail(IDOLQ_EINVAL, "w and out must be 4-byte aligned");
+    const int64_t total = idolq_q8_0_tiled_bytes(n, k) / 4;
+    hipLaunchKernelGGL(q8_tile_kernel, dim3(grid_for(total)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       reinterpret_cast<const uint32_t*>(w), n, (k / kQ8Block) * kQ8Bytes / 4, (int)(k / 64), total,
+                       reinterpret_cast<uint32_t*>(out));
+    return check_launch("q8_tile_kernel");
+}
+
 extern "C" int idolq_q8_0_quantize(const float* w, int64_t n, int64_t k, int64_t ldw, uint8_t* out, void* stream) {
     if (n < 0 || k <= 0 || k % kQ8Block || ldw < k) return fail(IDOLQ_EINVAL, "need n >= 0, k a positive multiple of 32, ldw >= k");
     const int64_t nb = k / kQ8Block, blocks = n * nb;

@@ -26,6 +26,7 @@ struct GemmParams {
     int tiles_m, tiles_n;
     int x_aligned;  // x rows are 16-byte aligned
     int y_vec;      // y (and the residual, when given) rows and base are 16-byte aligned: vector epilogue stores
+    int w_tiled;    // w is in the tiled layout (idolq_q8_0_tile), p.w at the window's first tile
     // INT8 mode
     const int8_t* qa;
     const float* sa;
@@ -50,9 +51,22 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, i
 }
 
 // The pipelined DEQUANT kernel (q8_gemm_pipe.hip): 256 x 128 tiles, 16-bit activations with 16-byte aligned rows,
-// k a multiple of 64 and a 4-byte aligned weight window.
+// k a multiple of 64 and a 4-byte aligned weight window. One persistent workgroup per CU; with a workspace of
+// pipe_workspace_bytes() the tiles' k stages are split evenly over the workgroups (stream-K).
 constexpr int kPipeBM = 256, kPipeBN = 128;
+
+struct PipeSplit {
+    int G;        // workgroups
+    int S;        // 64-deep stages per tile
+    int L, R;     // stream-K: workgroup r holds L + (r < R) stages
+    float* part;  // stream-K: G partial tiles (kPipeBM x kPipeBN fp32); null: whole tiles only
+    int* flags;   // G flags: workgroup r stores epoch when its partial tile is ready
+    int* error;   // set to 1 if a wait for a partial tile gave up
+    int epoch;    // launch number, never 0
+};
+
+size_t pipe_workspace_bytes();
 bool pipe_eligible(const GemmParams& p, int xt, int mode);
-int launch_pipe(GemmParams p, int xt, hipStream_t stream);
+int launch_pipe(GemmParams p, int xt, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 }  // namespace idolq

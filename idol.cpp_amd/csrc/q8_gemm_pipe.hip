@@ -22,6 +22,8 @@
 // loads need no masks; k is a multiple of 64, so there is no partial stage.
 #include "q8_gemm.h"
 
+#include <atomic>
+#include <string>
 #include <type_traits>
 
 namespace idolq {
@@ -180,41 +182,40 @@ __device__ __forceinline__ void epilogue_fast(const GemmParams& p, const f32x16 
     }
 }
 
-template <typename T>
-__global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, int vec4) {
+template <typename T, bool TILED>
+__global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, int vec4, PipeSplit sp) {
     typedef typename PipeMfma<T>::vec Vec;
     __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
-    int tile_m, tile_n;
-    tile_coords(p.tiles_m, p.tiles_n, tile_m, tile_n);
-    const int m0 = tile_m * kPipeBM, n0 = tile_n * kPipeBN;
-    const int nsteps = p.k / 64;
-
-    // ---- global -> LDS load offsets (bytes, 32-bit), fixed for the whole tile
+    // ---- global -> LDS load offsets (bytes, 32-bit) of the current tile, set by start_segment
     // activations: unit u = 512 j + tid (16 bytes) is LDS chunk u of the buffer: row u / 8, position u % 8, which
     // holds chunk (u % 8) ^ ((row >> 1) & 7) of the row's 128 bytes
-    uint32_t a_off[4];
-    {
+    // weights: dword unit u = 512 j + tid of the [128 rows][17 dwords] stage is LDS dword u
+    uint32_t a_off[4], w_off[5];
+    const char* xg;  // activations / weight bytes of the segment's first stage
+    const char* wg;
+    int nsteps;      // stages in the segment
+    auto start_segment = [&](int m0, int n0, int k0, int n) {
         const int r = tid >> 3, c = (tid & 7) ^ ((r >> 1) & 7);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int row = min(m0 + 64 * j + r, p.m - 1);
             a_off[j] = (uint32_t)((int64_t)row * p.ldx * 2 + c * 16);
         }
-    }
-    // weights: dword unit u = 512 j + tid of the [128 rows][17 dwords] stage is LDS dword u
-    uint32_t w_off[5];
 #pragma unroll
-    for (int j = 0; j < 5; ++j) {
-        const int u = min(512 * j + tid, kRawUnits - 1);
-        const int row = min(n0 + u / 17, p.n - 1);
-        w_off[j] = (uint32_t)((int64_t)row * p.row_bytes + (u % 17) * 4);
-    }
-    const char* xg = static_cast<const char*>(p.x);
-    const char* wg = reinterpret_cast<const char*>(p.w);
+        for (int j = 0; j < 5; ++j) {
+            const int u = min(512 * j + tid, kRawUnits - 1);
+            const int row = min(n0 + u / 17, p.n - 1);
+            w_off[j] = (uint32_t)((int64_t)row * p.row_bytes + (u % 17) * 4);
+        }
+        xg = static_cast<const char*>(p.x) + (size_t)k0 * 128;
+        wg = TILED ? reinterpret_cast<const char*>(p.w) + ((size_t)(n0 / kPipeBN) * (p.k / 64) + k0) * kRawBuf
+                   : reinterpret_cast<const char*>(p.w) + (size_t)k0 * 68;
+        nsteps = n;
+    };
 
     const uint32_t lds0 = (uint32_t)(size_t)(lds_char*)smem;
     auto issue_a = [&](int s) {
@@ -226,7 +227,18 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
     // 2176 dwords are 4.25 loads per wave: the fifth load of waves 2..7 reads a valid address into a junk area, so
     // every wave issues the same five loads (no branch, and the same vmcnt on every wave)
     const uint32_t w_dst4 = wave < (kRawUnits - 2048) / 64 ? kRawBase + 4 * 2048 + wave * 256 : kJunk;
+    // tiled weights: the stage's 8704 bytes are contiguous: 16 bytes per lane, 1 KB per wave, and the last 512 bytes
+    // by the first half of wave 0
+    auto issue_w_tiled_rest = [&](const char* base, int slot) {
+        if (wave == 0 && lane < 32) lds_dma16(base, (uint32_t)(8192 + lane * 16), lds0 + kRawBase + slot * kRawBuf + 8192);
+    };
     auto issue_w = [&](int s) {
+        if (TILED) {
+            const char* base = wg + (size_t)s * kRawBuf;
+            lds_dma16(base, (uint32_t)(tid * 16), lds0 + kRawBase + (s % 3) * kRawBuf + wave * 1024);
+            issue_w_tiled_rest(base, s % 3);
+            return;
+        }
         const char* base = wg + (size_t)s * 68;
         const uint32_t dst = lds0 + kRawBase + (s % 3) * kRawBuf + wave * 256;
 #pragma unroll
@@ -271,12 +283,6 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
     }
 
     f32x16 acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     // MFMA operands of one stage in registers, in four groups g = 2 blk + h (16 deep each): w[g][tn], x[g][tm]
     Vec ow[4][2], ox[4][2];
@@ -300,6 +306,14 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
 #pragma unroll
             for (int tn = 0; tn < 2; ++tn) acc[tm][tn] = PipeMfma<T>::run(ow[g][tn], ox[g][tm], acc[tm][tn]);
     };
+
+    auto run_segment = [&]() {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     // ---- prologue. At the start of stage s, stage s's operands are in registers, activations s + 1 and weights
     // s + 1 (converted) are in LDS, weight bytes s + 2 have landed, activations s + 2 and weight bytes s + 3 are in
@@ -339,13 +353,14 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
         char* bdst = smem + kBBase + (s & 1) * kBBuf + cv_row * kBPitch + cv_q * 16;
         const char* abase = xg + (size_t)(s + 3) * 128;
         const uint32_t adst = lds0 + ((s + 3) % 3) * kABuf + wave * 1024;
-        const char* wbase = wg + (size_t)(s + 4) * 68;
+        const char* wbase = wg + (size_t)(s + 4) * (TILED ? kRawBuf : 68);
         const int wslot = (s + 4) % 3;
-        const uint32_t wdst = lds0 + kRawBase + wslot * kRawBuf + wave * 256;
+        const uint32_t wdst = lds0 + kRawBase + wslot * kRawBuf + wave * (TILED ? 1024 : 256);
         uint2 q0, q1, q2, q3;
 #define IDOLQ_SEGMENT(G, WORK)                                     \
         lds_dma16(abase, a_off[G], adst + G * 8192);               \
-        lds_dma4(wbase, w_off[G], wdst + G * 2048);                \
+        if (!TILED) lds_dma4(wbase, w_off[G], wdst + G * 2048);    \
+        if (TILED && G == 0) lds_dma16(wbase, (uint32_t)(tid * 16), wdst); \
         mfma_group(G);                                             \
         read_group(s + 1, G);                                      \
         WORK;                                                      \
@@ -370,10 +385,15 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
         IDOLQ_SEGMENT(3, q3 = dequant4<T>(raw.b1, d1);
                          *reinterpret_cast<uint4*>(bdst + 64) = make_uint4(q2.x, q2.y, q3.x, q3.y));
 #undef IDOLQ_SEGMENT
-        lds_dma4(wbase, w_off[4], lds0 + w_dst4 + (w_dst4 == kJunk ? 0 : wslot * kRawBuf));
-        // activations s + 2 and weight bytes s + 3 (issued in stage s - 1) have landed once at most the 9 loads
-        // issued in this stage remain outstanding
-        wait_vm<9>();
+        if (!TILED) lds_dma4(wbase, w_off[4], lds0 + w_dst4 + (w_dst4 == kJunk ? 0 : wslot * kRawBuf));
+        if (TILED) issue_w_tiled_rest(wbase, wslot);
+        // activations s + 2 and weight bytes s + 3 (issued in stage s - 1) have landed once at most the loads issued
+        // in this stage remain outstanding: 4 + 5 (raw weights), 4 + 1 (tiled; wave 0 issues one more and waits for
+        // one of this stage's loads too)
+        if (TILED)
+            wait_vm<5>();
+        else
+            wait_vm<9>();
         __syncthreads();
     };
     auto stage_tail = [&](int s) {
@@ -394,8 +414,10 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
     int s = 0;
     for (; s < steady; ++s) stage_steady(s);
     for (; s < nsteps; ++s) stage_tail(s);
+    };
 
     // ---- epilogue from the registers
+    auto epilogue = [&](int m0, int n0) {
     const int row0 = m0 + wm * 64 + (lane & 31);
     const int col0 = n0 + wn * 64 + 4 * (lane >> 5);
     constexpr int kYdt = std::is_same<T, __bf16>::value ? IDOLQ_BF16 : IDOLQ_F16;
@@ -415,28 +437,183 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
         const int col = col0 + ((i >> 4) & 1) * 32 + 8 * (r >> 2) + (r & 3);
         if (row < p.m && col < p.n) epilogue_element(p, row, col, stash[i * kThreads + tid]);
     }
+    };
+
+    // ---- work: whole tiles (tiles r, r + G, ...) or, when sp.part is set, a contiguous range of the tiles' stages
+    // (stream-K): range r holds sp.L (+1 for r < sp.R) of the tiles * S stages in tile-major order, so every
+    // workgroup does the same work. A tile split across ranges is finished by the range holding its first stage:
+    // the ranges holding its other stages (each holds at most one such part: the first part of its range) store
+    // their fp32 partial tiles and raise their flags; the finishing range adds those partials before the epilogue.
+    int r = blockIdx.x;
+    if (sp.G % 8 == 0) r = (r % 8) * (sp.G / 8) + r / 8;  // ranges on one XCD are consecutive
+    const int ntiles = p.tiles_m * p.tiles_n;
+    auto tile_at = [&](int t, int& m0, int& n0) {
+        constexpr int G8 = 8;  // groups of 8 row-tiles, walked column by column
+        const int per_group = G8 * p.tiles_n, group = t / per_group, first = group * G8;
+        const int gm = min(p.tiles_m - first, G8), in_group = t - group * per_group;
+        m0 = (first + in_group % gm) * kPipeBM;
+        n0 = (in_group / gm) * kPipeBN;
+    };
+    if (sp.part == nullptr) {
+        for (int t = r; t < ntiles; t += sp.G) {
+            int m0, n0;
+            tile_at(t, m0, n0);
+            start_segment(m0, n0, 0, sp.S);
+            run_segment();
+            epilogue(m0, n0);
+            __syncthreads();
+        }
+        return;
+    }
+    const int64_t begin = (int64_t)r * sp.L + min(r, sp.R);
+    const int64_t end = begin + sp.L + (r < sp.R ? 1 : 0);
+    // range holding global stage index i
+    auto owner = [&](int64_t i) {
+        const int64_t big = (int64_t)sp.R * (sp.L + 1);
+        return (int)(i < big ? i / (sp.L + 1) : sp.R + (i - big) / sp.L);
+    };
+    // Partial tiles and flags are written and read with device-scope (relaxed atomic) accesses, which go to the
+    // memory-side coherence point instead of the XCD's L2: no L2 write-back or invalidation (which would also evict
+    // the tiles other workgroups are streaming) is needed to pass them between XCDs.
+    typedef unsigned long long u64;
+    u64* const part = reinterpret_cast<u64*>(sp.part);
+    constexpr int kPartU64 = kPipeBM * kPipeBN / 2;
+    for (int64_t i = begin; i < end;) {
+        const int t = (int)(i / sp.S), k0 = (int)(i % sp.S);
+        const int n = (int)min((int64_t)(sp.S - k0), end - i);
+        int m0, n0;
+        tile_at(t, m0, n0);
+        start_segment(m0, n0, k0, n);
+        run_segment();
+        if (k0 > 0) {
+            // a later part of the tile: store the partial accumulators (pair q of thread tid at q * 512 + tid), wait
+            // until they are written, then raise the flag
+#pragma unroll
+            for (int q = 0; q < 32; ++q) {
+                const f32x16& a = acc[q >> 4][(q >> 3) & 1];
+                const u64 v = ((u64)__float_as_uint(a[2 * (q & 7) + 1]) << 32) | __float_as_uint(a[2 * (q & 7)]);
+                __hip_atomic_store(part + (size_t)r * kPartU64 + q * kThreads + tid, v, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            }
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (tid == 0) __hip_atomic_store(sp.flags + r, sp.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            if (n < sp.S) {
+                // the tile's first part: wait for the ranges holding the rest, add their partials
+                const int last = owner((int64_t)(t + 1) * sp.S - 1);
+                if (tid == 0) {
+                    for (int c = r + 1; c <= last; ++c) {
+                        int spins = 0;
+                        while (__hip_atomic_load(sp.flags + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != sp.epoch) {
+                            __builtin_amdgcn_s_sleep(4);
+                            if (++spins > (1 << 22)) {  // never expected: give up rather than hang
+                                __hip_atomic_store(sp.error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                                break;
+                            }
+                        }
+                    }
+                }
+                __syncthreads();
+                for (int c = r + 1; c <= last; ++c) {
+#pragma unroll
+                    for (int q = 0; q < 32; ++q) {
+                        const u64 v = __hip_atomic_load(part + (size_t)c * kPartU64 + q * kThreads + tid, __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT);
+                        f32x16& a = acc[q >> 4][(q >> 3) & 1];
+                        a[2 * (q & 7)] += __uint_as_float((unsigned)v);
+                        a[2 * (q & 7) + 1] += __uint_as_float((unsigned)(v >> 32));
+                    }
+                }
+            }
+            epilogue(m0, n0);
+        }
+        __syncthreads();
+        i += n;
+    }
 }
 
 }  // namespace
 
 bool pipe_eligible(const GemmParams& p, int xt, int mode) {
     return mode == MODE_DEQUANT && (xt == XT_BF16 || xt == XT_F16) && p.x_aligned && p.k % 64 == 0 &&
-           p.row_bytes % 4 == 0 && (reinterpret_cast<uintptr_t>(p.w) & 3) == 0 &&
+           p.row_bytes % 4 == 0 && (reinterpret_cast<uintptr_t>(p.w) & (p.w_tiled ? 15 : 3)) == 0 &&
            (int64_t)p.m * p.ldx * 2 < (int64_t)UINT32_MAX && (int64_t)p.n * p.row_bytes < (int64_t)UINT32_MAX;
 }
 
-int launch_pipe(GemmParams p, int xt, hipStream_t stream) {
+namespace {
+int cu_count() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+std::atomic<int> g_epoch{0};
+}  // namespace
+
+// Partial tiles, flags and the error word for one workgroup per CU.
+size_t pipe_workspace_bytes() {
+    const size_t g = (size_t)cu_count();
+    return g * kPipeBM * kPipeBN * sizeof(float) + g * sizeof(int) + 256;
+}
+
+int launch_pipe(GemmParams p, int xt, void* workspace, size_t workspace_bytes, hipStream_t stream) {
     p.tiles_m = (p.m + kPipeBM - 1) / kPipeBM;
     p.tiles_n = (p.n + kPipeBN - 1) / kPipeBN;
     // 4-element groups of y, the residual and the bias are vector-accessible
     int vec4 = reinterpret_cast<uintptr_t>(p.y) % (4 * dtype_size(p.y_dt)) == 0 && p.ldy % 4 == 0;
     if (p.res) vec4 = vec4 && reinterpret_cast<uintptr_t>(p.res) % (4 * dtype_size(p.res_dt)) == 0 && p.ldr % 4 == 0;
     if (p.bias) vec4 = vec4 && reinterpret_cast<uintptr_t>(p.bias) % (4 * dtype_size(p.bias_dt)) == 0;
-    const dim3 grid(p.tiles_m * p.tiles_n), block(kThreads);
-    if (xt == XT_BF16)
-        hipLaunchKernelGGL(q8_gemm_pipe_kernel<__bf16>, grid, block, 0, stream, p, vec4);
-    else
-        hipLaunchKernelGGL(q8_gemm_pipe_kernel<_Float16>, grid, block, 0, stream, p, vec4);
+
+    const int cus = cu_count();
+    const int tiles = p.tiles_m * p.tiles_n, S = p.k / 64;
+    const int64_t total = (int64_t)tiles * S;
+    PipeSplit sp{};
+    sp.S = S;
+    // stream-K when the tiles do not fill whole rounds of the CUs and a workspace is given
+    const bool split = workspace && workspace_bytes >= pipe_workspace_bytes() &&
+                       reinterpret_cast<uintptr_t>(workspace) % 256 == 0 && tiles % cus != 0 && total >= cus &&
+                       total / cus < INT32_MAX;
+    if (split) {
+        sp.G = cus;
+        sp.L = (int)(total / cus);
+        sp.R = (int)(total % cus);
+        sp.part = static_cast<float*>(workspace);
+        sp.flags = reinterpret_cast<int*>(static_cast<char*>(workspace) + (size_t)cus * kPipeBM * kPipeBN * sizeof(float));
+        sp.error = sp.flags + cus;
+        int e = g_epoch.fetch_add(1) + 1;
+        if (e <= 0) {  // wrapped: restart at 1
+            g_epoch.store(1);
+            e = 1;
+        }
+        sp.epoch = e;
+    } else {
+        sp.G = tiles < cus ? tiles : cus;
+    }
+    const dim3 grid(sp.G), block(kThreads);
+    void* fn = xt == XT_BF16 ? (p.w_tiled ? reinterpret_cast<void*>(&q8_gemm_pipe_kernel<__bf16, true>)
+                                          : reinterpret_cast<void*>(&q8_gemm_pipe_kernel<__bf16, false>))
+                             : (p.w_tiled ? reinterpret_cast<void*>(&q8_gemm_pipe_kernel<_Float16, true>)
+                                          : reinterpret_cast<void*>(&q8_gemm_pipe_kernel<_Float16, false>));
+    if (split) {
+        // a workgroup may wait for a later one: all must be resident at once
+        void* args[] = {&p, &vec4, &sp};
+        const hipError_t e = hipLaunchCooperativeKernel(fn, grid, block, args, 0, stream);
+        if (e != hipSuccess) return fail(IDOLQ_ELAUNCH, std::string("q8_gemm_pipe_kernel: ") + hipGetErrorString(e));
+        return check_launch("q8_gemm_pipe_kernel");
+    }
+#define IDOLQ_LAUNCH_PIPE(TT, TILED) hipLaunchKernelGGL((q8_gemm_pipe_kernel<TT, TILED>), grid, block, 0, stream, p, vec4, sp)
+    if (xt == XT_BF16) {
+        if (p.w_tiled) IDOLQ_LAUNCH_PIPE(__bf16, true); else IDOLQ_LAUNCH_PIPE(__bf16, false);
+    } else {
+        if (p.w_tiled) IDOLQ_LAUNCH_PIPE(_Float16, true); else IDOLQ_LAUNCH_PIPE(_Float16, false);
+    }
+#undef IDOLQ_LAUNCH_PIPE
     return check_launch("q8_gemm_pipe_kernel");
 }
 

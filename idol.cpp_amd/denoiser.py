@@ -29,19 +29,25 @@ def _q8(gen, n, k, std, device):
 
 
 class DenoiserLayer:
-    """Q8_0 weights and fp32 biases of one layer."""
+    """Q8_0 weights (GGUF row-major blocks in `w`; the same blocks in the tiled GEMM layout in `wt`, made once at
+    build time) and fp32 biases of one layer."""
 
     def __init__(self, gen, device, dim=D, mlp=MLP, ctx_dim=CTX_DIM, wstd=0.02, bstd=0.01):
         self.dim, self.mlp, self.ctx_dim = dim, mlp, ctx_dim
         shapes = {"qkv": (3 * dim, dim), "out": (dim, dim), "cq": (dim, dim), "ckv": (2 * dim, ctx_dim),
                   "cout": (dim, dim), "up": (mlp, dim), "down": (dim, mlp)}
-        self.w, self.b, self.shape = {}, {}, shapes
+        self.w, self.wt, self.b, self.shape = {}, {}, {}, shapes
         for name, (n, k) in shapes.items():
             self.w[name] = _q8(gen, n, k, wstd, device)
             self.b[name] = torch.randn(n, device=device, generator=gen) * bstd
+            if k % 64 == 0:
+                self.wt[name] = L.tile_q8_0(self.w[name], n, k)
 
     def linear(self, name, x, out, act=L.ACT_NONE, residual=None, mode=L.MODE_DEQUANT):
         n, _ = self.shape[name]
+        if mode == L.MODE_DEQUANT and name in self.wt:
+            return L.gemm(x, self.wt[name], n, bias=self.b[name], act=act, residual=residual, mode=mode, out=out,
+                          tiled=True)
         return L.gemm(x, self.w[name], n, bias=self.b[name], act=act, residual=residual, mode=mode, out=out)
 
 

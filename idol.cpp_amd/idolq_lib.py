@@ -13,7 +13,7 @@ LIB_PATH = Path(__file__).resolve().parent / "lib" / "libidolq.so"
 F32, F16, BF16 = 0, 1, 2
 ACT_NONE, ACT_GELU_ERF, ACT_GELU_TANH, ACT_RELU = 0, 1, 2, 3
 MODE_AUTO, MODE_DEQUANT, MODE_EXACT, MODE_INT8 = 0, 1, 2, 3
-FLAG_ROUND_BEFORE_BIAS = 1
+FLAG_ROUND_BEFORE_BIAS, FLAG_TILED_WEIGHTS = 1, 2
 EINVAL, ELAUNCH, ENOSUPPORT = -1, -2, -3
 
 DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
@@ -30,6 +30,8 @@ _SIGNATURES = {
                                _int, _int, _vp, _int, _i64, _vp, _sz, _vp]),
     "idolq_q8_0_gemm_workspace": (_sz, [_i64, _i64, _int]),
     "idolq_q8_0_quantize": (_int, [_vp, _i64, _i64, _i64, _vp, _vp]),
+    "idolq_q8_0_tiled_bytes": (_i64, [_i64, _i64]),
+    "idolq_q8_0_tile": (_int, [_vp, _i64, _i64, _vp, _vp]),
     "idolq_q8_0_dequant": (_int, [_vp, _i64, _i64, _vp, _int, _vp]),
     "idolq_quantize_act_q8": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
     "idolq_q8_0_block_dots": (_int, [_vp, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _vp]),
@@ -116,9 +118,27 @@ def q8_0_bytes(n, k):
     return int(load().idolq_q8_0_bytes(n, k))
 
 
+_split_workspaces = {}
+
+
+def _split_workspace(device, nbytes):
+    """The zero-filled DEQUANT workspace of a device (partial tiles and flags of the split k stages), kept for the
+    process: the library leaves it ready for the next call. Calls on one device share it, so they must not overlap
+    (one stream)."""
+    ws = _split_workspaces.get(device)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(nbytes, device=device, dtype=torch.uint8)
+        _split_workspaces[device] = ws
+    return ws
+
+
 def gemm(x, w, n_total, n_offset=0, n=None, bias=None, residual=None, act=ACT_NONE, mode=MODE_AUTO, flags=0,
-         out=None, out_dtype=None, workspace=None):
-    """y = epilogue(x @ W[n_offset:n_offset+n]^T) with W raw Q8_0 blocks. x is [m, k] (unit-stride rows)."""
+         out=None, out_dtype=None, workspace=None, split=False, tiled=False):
+    """y = epilogue(x @ W[n_offset:n_offset+n]^T) with W Q8_0 blocks, row-major (GGUF) or, with tiled=True, in the
+    layout of tile_q8_0. x is [m, k] (unit-stride rows).
+
+    In DEQUANT mode split=True passes the device's cached workspace, which lets the library split the tiles' k range
+    over the CUs (partial tiles); by default whole tiles per workgroup."""
     lib = load()
     m, k = x.shape
     if n is None:
@@ -126,21 +146,44 @@ def gemm(x, w, n_total, n_offset=0, n=None, bias=None, residual=None, act=ACT_NO
     dev = _require_cuda(x, w, bias, residual, out, workspace)
     if w.dtype != torch.uint8:
         raise ValueError("Q8_0 weights are a uint8 tensor")
-    if w.numel() != q8_0_bytes(n_total, k) or not w.is_contiguous():
+    wbytes = int(lib.idolq_q8_0_tiled_bytes(n_total, k)) if tiled else q8_0_bytes(n_total, k)
+    if w.numel() != wbytes or not w.is_contiguous():
         raise ValueError("Q8_0 weight size does not match its shape")
+    if tiled:
+        flags |= FLAG_TILED_WEIGHTS
     if out is None:
         out = torch.empty((m, n), device=x.device, dtype=out_dtype or x.dtype)
     if bias is not None and (bias.dim() != 1 or bias.numel() != n_total or not bias.is_contiguous()):
         raise ValueError("bias must be a contiguous vector of n_total values")
-    ws_bytes = int(lib.idolq_q8_0_gemm_workspace(m, k, mode))
+    eff_mode = mode if mode != MODE_AUTO else (MODE_EXACT if x.dtype == torch.float32 else MODE_DEQUANT)
+    ws_bytes = int(lib.idolq_q8_0_gemm_workspace(m, k, eff_mode))
     if ws_bytes and (workspace is None or workspace.numel() * workspace.element_size() < ws_bytes):
-        workspace = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8)
+        if eff_mode == MODE_DEQUANT:
+            workspace = _split_workspace(x.device, ws_bytes) if split else None
+        else:
+            workspace = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8)
     ldr = _row_stride(residual) if residual is not None else 0
     _check(lib.idolq_q8_0_gemm(_ptr(x), _code(x), m, k, _row_stride(x), _ptr(w), n_total, n_offset, n, _ptr(bias),
                                _code(bias) if bias is not None else 0, _ptr(residual),
                                _code(residual) if residual is not None else 0, ldr, act, mode, flags, _ptr(out),
-                               _code(out), _row_stride(out), _ptr(workspace) if ws_bytes else None, ws_bytes,
+                               _code(out), _row_stride(out), _ptr(workspace) if workspace is not None else None,
+                               ws_bytes if workspace is not None else 0,
                                _stream(dev)))
+    return out
+
+
+def tile_q8_0(w, n, k):
+    """The tiled layout (idolq_q8_0_tile) of GGUF Q8_0 blocks of an [n, k] weight: the same blocks, reordered once so
+    that each GEMM stage reads contiguous bytes. Needs k % 64 == 0."""
+    lib = load()
+    _require_cuda(w)
+    if w.dtype != torch.uint8 or w.numel() != q8_0_bytes(n, k) or not w.is_contiguous():
+        raise ValueError("Q8_0 weight size does not match its shape")
+    nbytes = int(lib.idolq_q8_0_tiled_bytes(n, k))
+    if nbytes == 0:
+        raise ValueError("the tiled layout needs k a multiple of 64")
+    out = torch.empty(nbytes, device=w.device, dtype=torch.uint8)
+    _check(lib.idolq_q8_0_tile(_ptr(w), n, k, _ptr(out), _stream(w.device)))
     return out
 
 

@@ -36,8 +36,9 @@ enum { IDOLQ_ACT_NONE = 0, IDOLQ_ACT_GELU_ERF = 1, IDOLQ_ACT_GELU_TANH = 2, IDOL
 enum { IDOLQ_MODE_AUTO = 0, IDOLQ_MODE_DEQUANT = 1, IDOLQ_MODE_EXACT = 2, IDOLQ_MODE_INT8 = 3 };
 
 /* GEMM flags. ROUND_BEFORE_BIAS rounds the product to the output dtype before the bias is added, as the reference's
- * fused GPU path does (tools/idol_triton.py:84-89). */
-enum { IDOLQ_FLAG_ROUND_BEFORE_BIAS = 1 };
+ * fused GPU path does (tools/idol_triton.py:84-89). TILED_WEIGHTS: w is in the tiled Q8_0 layout written by
+ * idolq_q8_0_tile (DEQUANT mode, bf16/fp16 activations with 16-byte aligned rows, k % 64 == 0, n_offset % 128 == 0). */
+enum { IDOLQ_FLAG_ROUND_BEFORE_BIAS = 1, IDOLQ_FLAG_TILED_WEIGHTS = 2 };
 
 enum {
     IDOLQ_OK = 0,
@@ -63,7 +64,10 @@ int64_t idolq_q8_0_bytes(int64_t n, int64_t k);
  *   residual NULL or [m x n] in residual_dtype, row stride ldr; may alias y (same dtype and stride)
  *   act      IDOLQ_ACT_*, applied after bias and residual
  *   y        [m x n] in y_dtype, row stride ldy
- *   workspace / workspace_bytes  scratch for IDOLQ_MODE_INT8 (idolq_q8_0_gemm_workspace bytes), else may be NULL
+ *   workspace / workspace_bytes  scratch of idolq_q8_0_gemm_workspace bytes: required by IDOLQ_MODE_INT8 (quantized
+ *            activations); optional for IDOLQ_MODE_DEQUANT, where it lets the k stages of the tiles be split evenly
+ *            over the CUs (partial tiles and flags). A DEQUANT workspace must be zero-filled before its first use
+ *            and used by one stream at a time; calls leave it ready for the next call.
  * Replaces src/kernels.hpp:73-76 gemm_packed (fp32 x, residual before GELU, column window n_offset / n) and
  * tools/idol_triton.py:94-126 fused_linear (bf16/fp16 x, bias after rounding: IDOLQ_FLAG_ROUND_BEFORE_BIAS). */
 int idolq_q8_0_gemm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* w, int64_t n_total,
@@ -71,13 +75,23 @@ int idolq_q8_0_gemm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ld
                     int residual_dtype, int64_t ldr, int act, int mode, int flags, void* y, int y_dtype, int64_t ldy,
                     void* workspace, size_t workspace_bytes, void* stream);
 
-/* Workspace bytes idolq_q8_0_gemm needs for m rows of depth k in the given mode (0 except for IDOLQ_MODE_INT8). */
+/* Workspace bytes idolq_q8_0_gemm uses for m rows of depth k in the given mode: the quantized activations for
+ * IDOLQ_MODE_INT8, the partial tiles of the current device's CUs for IDOLQ_MODE_DEQUANT, 0 for IDOLQ_MODE_EXACT. */
 size_t idolq_q8_0_gemm_workspace(int64_t m, int64_t k, int mode);
 
 /* Quantizes an fp32 [n x k] matrix (row stride ldw) to Q8_0 blocks: per 32 values d = amax / 127,
  * q = round-half-away-from-zero(x * (1 / d)), d stored as fp16. The rule of ggml's quantize_row_q8_0_ref, which
  * gguf-py's quantize(..., Q8_0) restates (tools/export_full_gguf.py:332-335, tests/python/test_fused_packed.py:40). */
 int idolq_q8_0_quantize(const float* w, int64_t n, int64_t k, int64_t ldw, uint8_t* out, void* stream);
+
+/* Tiled Q8_0: the same 34-byte blocks, reordered once (at load time) so that the bytes one GEMM stage reads are
+ * contiguous. Rows are grouped in tiles of 128 (the last tile padded with zero blocks) and k in stages of 64 (two
+ * blocks); chunk (t, s) = the 68 bytes of stage s of each of the 128 rows of tile t, row after row (8704 bytes), at
+ * byte (t * (k / 64) + s) * 8704. Needs k % 64 == 0 (else the size is 0 / EINVAL). Layout of this library only: the
+ * reference keeps GGUF blocks row-major (tools/idol_packed.py:28-31) and its CPU kernels use 16-column panels
+ * (src/kernels.hpp:33-51). */
+int64_t idolq_q8_0_tiled_bytes(int64_t n, int64_t k);
+int idolq_q8_0_tile(const uint8_t* w, int64_t n, int64_t k, uint8_t* out, void* stream);
 
 /* out[r, c] = out_dtype(fp32(d) * q) for the whole [n x k] weight, out row stride k.
  * Replaces tools/idol_triton.py:24-33 _unpack_q8 and tools/idol_packed.py:25-31,71 PackedLinear.dequantize. */

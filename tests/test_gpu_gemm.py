@@ -188,3 +188,57 @@ def test_empty_and_tiny_inputs():
     # fp32 activations (2^-16 of each term) against the sum of the terms' magnitudes
     terms = np.abs(a[0] * O.q8_0_dequant(w, 7, 64)[3]).sum()
     assert norm_rel(y, ref) < 1e-3 and abs(float(y[0, 0] - ref[0, 0])) <= terms * 2.0 ** -16
+
+
+@pytest.mark.parametrize("m,n,k", [(1024, 1536, 2048), (512, 384, 1280), (4096, 1536, 6144), (300, 520, 3072)])
+def test_split_k_matches_whole_tiles(m, n, k):
+    # DEQUANT with the k stages of the tiles split over the CUs (partial tiles summed through the workspace) against
+    # whole tiles per workgroup: the same products summed in another order (fp32), so within 1e-5 norm-relative before
+    # the bf16 output rounding; both within 1e-3 of an fp32 product of the dequantized weights. Three calls in a row
+    # give identical results (the workspace flags carry over between calls).
+    rng = np.random.default_rng(m + n + k)
+    w = to_dev(q8(rng, n, k))
+    x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(DEV).bfloat16()
+    b = torch.from_numpy(rng.normal(0, 0.01, n).astype(np.float32)).to(DEV)
+    whole = L.gemm(x, w, n, bias=b, mode=L.MODE_DEQUANT, out_dtype=torch.float32, split=False)
+    runs = [L.gemm(x, w, n, bias=b, mode=L.MODE_DEQUANT, out_dtype=torch.float32, split=True) for _ in range(3)]
+    torch.cuda.synchronize()
+    assert torch.equal(runs[0], runs[1]) and torch.equal(runs[1], runs[2])
+    assert norm_rel(runs[0].cpu().numpy(), whole.cpu().numpy()) < 1e-5
+    ref = x.float() @ L.dequant(w, n, k, torch.bfloat16).float().T + b
+    assert norm_rel(runs[0].cpu().numpy(), ref.cpu().numpy()) < 1e-3
+    ws = L._split_workspaces[x.device]
+    nbytes = int(L.load().idolq_q8_0_gemm_workspace(m, k, L.MODE_DEQUANT))
+    assert int(ws[nbytes - 256:nbytes - 252].view(torch.int32).item()) == 0  # no wait gave up
+
+
+def tiled_layout(blocks, n, k):
+    """The tiled Q8_0 layout restated in numpy: chunk (t, s) = 68 bytes of stage s of each of rows 128 t .. 128 t + 127
+    (zero rows past n), chunks tile-major."""
+    S = k // 64
+    raw = blocks.reshape(n, S, 68)
+    nt = (n + 127) // 128
+    pad = np.zeros((nt * 128, S, 68), np.uint8)
+    pad[:n] = raw
+    return pad.reshape(nt, 128, S, 68).transpose(0, 2, 1, 3).reshape(-1)
+
+
+@pytest.mark.parametrize("m,n,k,off,cnt", [(256, 128, 64, 0, 128), (300, 200, 192, 128, 72), (1000, 1536, 1536, 0, 1536),
+                                         (513, 4608, 1280, 1536, 1536)])
+def test_tiled_weights_match_row_major(m, n, k, off, cnt):
+    # the tiled layout is a pure reordering of the blocks (bit-exact against the numpy restatement), and the GEMM on it
+    # gives bit-identical results to the GEMM on the row-major blocks (same kernel arithmetic)
+    rng = np.random.default_rng(m * 7 + n)
+    wq = q8(rng, n, k)
+    w = to_dev(wq)
+    wt = L.tile_q8_0(w, n, k)
+    assert np.array_equal(wt.cpu().numpy(), tiled_layout(wq, n, k))
+    x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(DEV).bfloat16()
+    b = torch.from_numpy(rng.normal(0, 0.01, n).astype(np.float32)).to(DEV)
+    res = torch.from_numpy(rng.standard_normal((m, cnt)).astype(np.float32)).to(DEV).bfloat16()
+    for act in (L.ACT_NONE, L.ACT_GELU_TANH):
+        raw = L.gemm(x, w, n, off, cnt, bias=b, residual=res, act=act, mode=L.MODE_DEQUANT)
+        til = L.gemm(x, wt, n, off, cnt, bias=b, residual=res, act=act, mode=L.MODE_DEQUANT, tiled=True)
+        assert torch.equal(raw, til)
+    with pytest.raises(ValueError):
+        L.gemm(x, wt, n, 64, 64, mode=L.MODE_DEQUANT, tiled=True)  # window not on a 128-row tile

@@ -46,7 +46,9 @@ def test_c_abi_rejects_bad_arguments_on_the_host():
     lib = L.load()
     assert lib.idolq_q8_0_bytes(6144, 1536) == 6144 * 48 * 34
     assert lib.idolq_q8_0_bytes(10, 33) == 0
-    assert lib.idolq_q8_0_gemm_workspace(4096, 1536, L.MODE_DEQUANT) == 0
+    assert lib.idolq_q8_0_gemm_workspace(4096, 1536, L.MODE_EXACT) == 0
+    # DEQUANT: one 256 x 128 fp32 partial tile and a flag per CU (256 where no device is visible), and an error word
+    assert lib.idolq_q8_0_gemm_workspace(4096, 1536, L.MODE_DEQUANT) >= 256 * (256 * 128 * 4 + 4)
     assert lib.idolq_q8_0_gemm_workspace(4096, 1536, L.MODE_INT8) >= 4096 * 1536 + 4096 * 48 * 4
     fake = ctypes.c_void_p(0x1000)  # never dereferenced: every call below fails its checks first
     rc = lib.idolq_q8_0_gemm(None, L.BF16, 4, 64, 64, fake, 8, 0, 8, None, 0, None, 0, 0, 0, 0, 0, fake, L.BF16, 8,
