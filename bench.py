@@ -47,6 +47,7 @@ def parse():
                         "MFMA with per-block fp32 scaling, or int8 MFMA on quantized activations")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-denoiser", action="store_true")
+    p.add_argument("--no-decoder-mlp", action="store_true")
     p.add_argument("--denoiser-layers", type=int, default=24)
     p.add_argument("--cpu-rows", type=int, default=1024, help="rows of the MLP block the CPU baseline runs")
     p.add_argument("--traffic-probe", action="store_true",
@@ -211,6 +212,72 @@ def run_denoiser(args):
     return out, model, ctx
 
 
+DECODER_POINTS = 262144
+
+
+def run_decoder_mlp(args):
+    """The decoders' tall-skinny per-point MLP (352 -> 256 -> 256 -> 64 Q8_0 with ReLU, fp32 64 -> 14 head) on 262144
+    points: ms per pass, GB/s of the bytes a fused pass must move (fp32 features, coordinates and outputs), TFLOP/s."""
+    import torch
+    import decoder_mlp
+
+    model = decoder_mlp.PointMLP(seed=0)
+    feats, coords = decoder_mlp.inputs(DECODER_POINTS, seed=1)
+    for _ in range(3):
+        model.forward(feats, coords)
+    torch.cuda.synchronize()
+    reps = 20
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        model.forward(feats, coords)
+    stop.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / reps
+    out = {"decoder_mlp_ms": round(ms, 4), "decoder_mlp_points": DECODER_POINTS,
+           "decoder_mlp_gbs": round(model.min_bytes(DECODER_POINTS) / (ms * 1e-3) / 1e9, 1),
+           "decoder_mlp_tflops": round(model.flop(DECODER_POINTS) / (ms * 1e-3) / 1e12, 2)}
+    return out, model
+
+
+def run_cpu_decoder_mlp(model, sample=16384):
+    """The reference's CPU kernels (oracle/_ref: gemm_packed float kernel on the three Q8_0 layers, dense gemm_packed
+    head; the position embedding from the oracle) on `sample` points, all host cores; scaled to 262144 points."""
+    import numpy as np
+    import torch
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle as O
+    import decoder_mlp
+
+    if not O.ref_available():
+        return {}
+    feats, coords = decoder_mlp.inputs(sample, seed=2)
+    f, c = feats.cpu().numpy(), coords.cpu().numpy()
+    blobs = {k: O.q8_0_to_panel(v.cpu().numpy(), *model.shape[k]) for k, v in model.w.items()}
+    b = {k: v.cpu().numpy() for k, v in model.b.items()}
+    hw, hb = model.head_w.cpu().numpy(), model.head_b.cpu().numpy()
+    freqs = model.freqs.cpu().numpy()
+
+    def run():
+        h = np.concatenate([f, O.pos_embed(freqs, c)], axis=1)
+        for name in ("l1", "l2", "l3"):
+            n, k = model.shape[name]
+            h = np.maximum(O.ref_gemm_panel(h, blobs[name], b[name], n, k, mode=0), 0.0)
+        return O.ref_gemm_dense(h, hw, hb)
+
+    run()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times)) * DECODER_POINTS / sample
+    cores = int(os.environ.get("OMP_NUM_THREADS", 0)) or os.cpu_count()
+    return {"decoder_mlp_cpu_ms_est": round(t * 1e3, 2), "decoder_mlp_cpu_cores": cores,
+            "decoder_mlp_cpu_note": f"reference kernels.cpp float kernel (3 Q8_0 layers) + dense head on {sample} "
+                                    f"points, median of 3 after 1 warm-up, scaled to {DECODER_POINTS} points"}
+
+
 def run_cpu_denoiser_layer(model, ctx):
     """The reference's CPU kernels (oracle/_ref: gemm_packed float kernel, norm_rows, attention, gelu_tanh) on one
     full-size denoiser layer, all host cores; the step estimate is 24 x the layer."""
@@ -328,6 +395,10 @@ def main():
         "roofline": gpu["roofline"],
         "pct_int8_peak": round(gpu["pct_int8_peak"], 4),
     }
+    dec_model = None
+    if not args.no_decoder_mlp:
+        dec, dec_model = run_decoder_mlp(args)
+        result.update(dec)
     model = ctx = None
     if not args.no_denoiser:
         dn, model, ctx = run_denoiser(args)
@@ -339,6 +410,11 @@ def main():
             result.update(cpu)
             if cpu:
                 result["denoiser_speedup_vs_cpu"] = round(cpu["denoiser_cpu_step_ms_est"] / result["denoiser_step_ms"], 1)
+        if dec_model is not None:
+            cpu = run_cpu_decoder_mlp(dec_model)
+            result.update(cpu)
+            if cpu:
+                result["decoder_mlp_speedup_vs_cpu"] = round(cpu["decoder_mlp_cpu_ms_est"] / result["decoder_mlp_ms"], 1)
     print(json.dumps(result), flush=True)
 
 

@@ -31,6 +31,7 @@ _SIGNATURES = {
     "idolq_q8_0_gemm_workspace": (_sz, [_i64, _i64, _int]),
     "idolq_q8_0_quantize": (_int, [_vp, _i64, _i64, _i64, _vp, _vp]),
     "idolq_q8_0_tiled_bytes": (_i64, [_i64, _i64]),
+    "idolq_linear_f32": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _i64, _vp, _int, _vp, _int, _i64, _vp]),
     "idolq_q8_0_tile": (_int, [_vp, _i64, _i64, _vp, _vp]),
     "idolq_q8_0_dequant": (_int, [_vp, _i64, _i64, _vp, _int, _vp]),
     "idolq_quantize_act_q8": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
@@ -184,6 +185,23 @@ def tile_q8_0(w, n, k):
         raise ValueError("the tiled layout needs k a multiple of 64")
     out = torch.empty(nbytes, device=w.device, dtype=torch.uint8)
     _check(lib.idolq_q8_0_tile(_ptr(w), n, k, _ptr(out), _stream(w.device)))
+    return out
+
+
+def linear_f32(x, w, bias=None, act=ACT_NONE, out=None, out_dtype=None):
+    """Dense fp32 layer y = act(x @ w^T + bias) (narrow heads: n <= 32); x [m, k] any float dtype, w [n, k] fp32."""
+    lib = load()
+    dev = _require_cuda(x, w, bias, out)
+    m, k = x.shape
+    n = w.shape[0]
+    if w.dtype != torch.float32 or w.shape[1] != k or not w.is_contiguous():
+        raise ValueError("w must be a contiguous fp32 [n, k] matrix")
+    if bias is not None and (bias.dtype != torch.float32 or bias.numel() != n or not bias.is_contiguous()):
+        raise ValueError("bias must be n contiguous fp32 values")
+    if out is None:
+        out = torch.empty((m, n), device=x.device, dtype=out_dtype or torch.float32)
+    _check(lib.idolq_linear_f32(_ptr(x), _code(x), m, k, _row_stride(x), _ptr(w), n, _ptr(bias), act, _ptr(out),
+                                _code(out), _row_stride(out), _stream(dev)))
     return out
 
 

@@ -140,6 +140,13 @@ int idolq_activation(void* x, int dtype, int64_t count, int act, void* stream);
 int idolq_pos_embed(const float* coords, int64_t rows, const float* freqs, int64_t nfreq, void* out, int out_dtype,
                     int64_t ldo, void* stream);
 
+/* Dense fp32 linear y[m x n] = act(x[m x k] * w^T + bias) for narrow layers (n <= 32, n * k <= 16384; else
+ * IDOLQ_ENOSUPPORT): the fp32 heads of the decoders' per-point MLPs. w [n x k] fp32 row-major, bias NULL or [n] fp32.
+ * Sums the depth in 32-deep FMA chunks added left to right, then adds the bias: bit-identical to the reference's
+ * dense gemm_packed (src/kernels.hpp:73-76 with an unquantized PackedLinear, src/kernels.cpp:566-596). */
+int idolq_linear_f32(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const float* w, int64_t n,
+                     const float* bias, int act, void* y, int y_dtype, int64_t ldy, void* stream);
+
 /* Copies a [rows x cols] block between dtypes and strides (a column slice of a wider row is a pointer offset). */
 int idolq_copy2d(const void* src, int src_dtype, int64_t lds, void* dst, int dst_dtype, int64_t ldd, int64_t rows,
                  int64_t cols, void* stream);

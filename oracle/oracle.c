@@ -277,6 +277,29 @@ void orc_gemm_q8_float(const float* a, int64_t m, const uint8_t* w, int64_t n_to
     }
 }
 
+/* src/kernels.cpp:566-596 (gemm_packed, unquantized PackedLinear): dense fp32 weights [n_total x k], the same
+ * 32-deep chunked FMA summation as the quantized float kernel, then finish_tile. */
+void orc_gemm_dense(const float* a, int64_t m, const float* w, int64_t n_total, int64_t k, const float* bias,
+                    int64_t n_offset, int64_t n, int gelu, float* c) {
+    (void)n_total;
+    const int64_t total = m * n;
+#pragma omp parallel for schedule(static)
+    for (int64_t idx = 0; idx < total; ++idx) {
+        const int64_t i = idx / n, j = idx % n;
+        const float* arow = a + i * k;
+        const float* wrow = w + (n_offset + j) * k;
+        float tile = 0.0f;
+        for (int64_t k0 = 0; k0 < k; k0 += 32) {
+            const int64_t kc = k - k0 < 32 ? k - k0 : 32;
+            float part = 0.0f;
+            for (int64_t t = 0; t < kc; ++t) part = fmaf(arow[k0 + t], wrow[k0 + t], part);
+            tile = k0 == 0 ? part : tile + part;
+        }
+        const int full = (j / 16) * 16 + 16 <= n;
+        c[idx] = finish(tile, bias ? bias[n_offset + j] : 0.0f, NULL, gelu, full);
+    }
+}
+
 /* src/kernels.cpp:368-404 (quantize_activations) for group 32: amax, s = amax / 127, inv = 127 / amax (0 when
  * amax == 0), q = round-to-nearest-even(x * inv) as int8, qsum = sum of q. */
 void orc_quantize_act(const float* a, int64_t m, int64_t k, int8_t* qa, float* scale, int32_t* qsum) {

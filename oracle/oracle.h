@@ -16,6 +16,7 @@
  *                                           codes of gguf-py 0.19.0 are PARITY UNPINNED (gguf is not installed)
  *   orc_q8_0_dequant, orc_q8_0_to_panel     closed form w = fp32(d)*q; reference dequantize_linear on the panel
  *   orc_gemm_q8_float                       reference gemm_packed (float kernel) golden vectors, bit-exact
+ *   orc_gemm_dense                          reference gemm_packed on dense fp32 weights (live build), bit-exact
  *   orc_quantize_act, orc_gemm_q8_int8      reference quantize_activations / gemm_packed (int8 kernel), bit-exact
  *   orc_layer_norm, orc_norm_rows           reference layer_norm / norm_rows, bit-exact
  *   orc_attention                           reference attention (blocked and dot paths), bit-exact
@@ -53,6 +54,9 @@ enum { ORC_ACT_NONE = 0, ORC_ACT_GELU_ERF = 1, ORC_ACT_GELU_TANH = 2, ORC_ACT_RE
  * applies the reference's erf-GELU after the residual. Float kernel semantics. */
 void orc_gemm_q8_float(const float* a, int64_t m, const uint8_t* w, int64_t n_total, int64_t k, const float* bias,
                        int64_t n_offset, int64_t n, const float* residual, int gelu, float* c);
+/* Dense fp32 weights [n_total x k] (an unquantized layer), same chunked summation and epilogue (no residual). */
+void orc_gemm_dense(const float* a, int64_t m, const float* w, int64_t n_total, int64_t k, const float* bias,
+                    int64_t n_offset, int64_t n, int gelu, float* c);
 /* Integer kernel semantics: activations quantized per row and 32-group, int32 block dots, per-group fold. */
 void orc_quantize_act(const float* a, int64_t m, int64_t k, int8_t* qa, float* scale, int32_t* qsum);
 void orc_gemm_q8_int8(const float* a, int64_t m, const uint8_t* w, int64_t n_total, int64_t k, const float* bias,

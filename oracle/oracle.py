@@ -58,6 +58,7 @@ def oracle_lib():
         gemm_args = [_f32p, _i64, _u8p, _i64, _i64, _vp, _i64, _i64, _vp, _int, _f32p]
         lib.orc_gemm_q8_float.argtypes = gemm_args
         lib.orc_gemm_q8_int8.argtypes = gemm_args
+        lib.orc_gemm_dense.argtypes = [_f32p, _i64, _f32p, _i64, _i64, _vp, _i64, _i64, _int, _f32p]
         lib.orc_quantize_act.argtypes = [_f32p, _i64, _i64, _i8p, _f32p, _i32p]
         lib.orc_block_dots.argtypes = [_i8p, _i64, _u8p, _i64, _i64, _i64, _i32p]
         lib.orc_layer_norm.argtypes = [_f32p, _i64, _i64, _f32p, _f32p, _f32p]
@@ -164,6 +165,17 @@ def _gemm(fn, a, w, n_total, k, bias, n_offset, n, residual, gelu):
 def gemm_q8_float(a, w, n_total, k, bias=None, n_offset=0, n=None, residual=None, gelu=False):
     """Reference float kernel semantics (gemm_packed, IDOL_QUANT_KERNEL=float) on Q8_0 blocks."""
     return _gemm(oracle_lib().orc_gemm_q8_float, a, w, n_total, k, bias, n_offset, n, residual, gelu)
+
+
+def gemm_dense(a, weight, bias=None, gelu=False):
+    """Reference dense gemm_packed semantics (unquantized fp32 weight [n, k]): 32-deep chunked FMA sums."""
+    a, weight = _f32(a), _f32(weight)
+    m, k = a.shape
+    n = weight.shape[0]
+    c = np.empty((m, n), np.float32)
+    b = _f32(bias) if bias is not None else None
+    oracle_lib().orc_gemm_dense(a, m, weight, n, k, _ptr(b), 0, n, int(gelu), c)
+    return c
 
 
 def gemm_q8_int8(a, w, n_total, k, bias=None, n_offset=0, n=None, residual=None, gelu=False):

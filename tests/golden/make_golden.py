@@ -5,7 +5,7 @@ src/decoders.cpp and src/weights.cpp where they lie, with the reference's flags,
 integer kernel). Inputs are seeded; each fixture stores its inputs and the reference outputs, so the tests need
 neither the reference checkout nor its build.
 
-    make -C oracle && python tests/golden/make_golden.py
+    make -C oracle && python tests/golden/make_golden.py [fixture names, default all]
 """
 import sys
 from pathlib import Path
@@ -31,6 +31,9 @@ GEMM_CASES = [
     (48, 256, 256, 32, 192, True, False),
 ]
 
+# (m, n, k, gelu): dense fp32 heads (src/kernels.cpp:566-596), the decoders' 64 -> 14 head among them, K tails.
+DENSE_CASES = [(300, 14, 64, False), (37, 5, 100, False), (64, 33, 352, True), (9, 1, 7, False), (40, 32, 512, True)]
+
 ATTN_CASES = [(5, 9, 3, 4), (37, 53, 2, 32), (3, 16, 1, 16), (70, 130, 2, 64), (40, 77, 3, 20), (64, 96, 2, 64)]
 
 
@@ -51,6 +54,19 @@ def gemm_fixture(rng):
         for key, val in case.items():
             out[f"c{i}_{key}"] = val
     out["cases"] = np.array(len(GEMM_CASES))
+    return out
+
+
+def gemm_dense_fixture(rng):
+    out = {}
+    for i, (m, n, k, gelu) in enumerate(DENSE_CASES):
+        w = rng.normal(0, 0.1, (n, k)).astype(np.float32)
+        a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+        bias = rng.uniform(-0.5, 0.5, n).astype(np.float32)
+        out[f"c{i}_shape"] = np.array([m, n, k, int(gelu)])
+        out[f"c{i}_a"], out[f"c{i}_w"], out[f"c{i}_bias"] = a, w, bias
+        out[f"c{i}_y"] = O.ref_gemm_dense(a, w, bias, gelu=gelu)
+    out["cases"] = np.array(len(DENSE_CASES))
     return out
 
 
@@ -111,7 +127,12 @@ def main():
         "attention": attention_fixture(rng),
         "elementwise": elementwise_fixture(rng),
     }
+    # added later with a seed of its own, so the fixtures above keep their bytes
+    fixtures["gemm_dense"] = gemm_dense_fixture(np.random.default_rng(20261202))
+    only = set(sys.argv[1:])
     for name, arrays in fixtures.items():
+        if only and name not in only:
+            continue
         path = HERE / f"{name}.npz"
         np.savez_compressed(path, **arrays)
         print(f"wrote {path.name}: {path.stat().st_size} bytes")

@@ -217,6 +217,35 @@ def test_float_gemm_column_window_adds_residual_before_exact_gelu():
     assert np.max(np.abs(y - exact)) < 1e-4
 
 
+def test_dense_gemm_sums_depth_in_32_deep_chunks():
+    # src/kernels.cpp:566-596: fp32 weights, depth in chunks of 32, each an FMA chain from zero, partials added left to
+    # right. Row [2^24, 1 x63] against unit weights (exact 2^24 + 63): the first chunk's 1s round away next to 2^24,
+    # the second chunk sums to 32 on its own, so 32-deep chunks give 2^24 + 32; one chain over the whole depth gives
+    # 2^24 and 16-deep chunks give 2^24 + 48.
+    a = np.ones((1, 64), np.float32)
+    a[0, 0] = 2.0 ** 24
+    w = np.ones((3, 64), np.float32)
+    assert np.array_equal(O.gemm_dense(a, w), np.full((1, 3), 2.0 ** 24 + 32, np.float32))
+    # bias after the depth sum; fp64 closeness with a ragged tail; exact erf-GELU after the bias
+    rng = np.random.default_rng(11)
+    for (m, n, k) in [(9, 14, 64), (5, 33, 100), (3, 1, 7)]:
+        a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+        w = rng.uniform(-0.5, 0.5, (n, k)).astype(np.float32)
+        bias = rng.uniform(-0.5, 0.5, n).astype(np.float32)
+        pre = a.astype(np.float64) @ w.T.astype(np.float64) + bias
+        assert np.max(np.abs(O.gemm_dense(a, w, bias) - pre)) < 1e-5
+        exact = 0.5 * pre * (1 + np.vectorize(math.erf)(pre / math.sqrt(2)))
+        assert np.max(np.abs(O.gemm_dense(a, w, bias, gelu=True) - exact)) < 1e-4
+
+
+def test_dense_gemm_matches_reference_golden_bit_for_bit(golden):
+    g = golden("gemm_dense")
+    for i in range(int(g["cases"])):
+        gelu = bool(g[f"c{i}_shape"][3])
+        y = O.gemm_dense(g[f"c{i}_a"], g[f"c{i}_w"], g[f"c{i}_bias"], gelu=gelu)
+        assert np.array_equal(bits(y), bits(g[f"c{i}_y"])), f"case {i}"
+
+
 def test_int8_gemm_identities_and_closeness_to_float():
     rng = np.random.default_rng(7)
     m, n, k = 19, 37, 256
@@ -346,6 +375,9 @@ def test_oracle_matches_live_reference_build_on_fresh_seeds():
             for gelu in (False, True):
                 ref = O.ref_gemm_panel(a, blob, bias, n, k, 0, n, None, gelu, mode=mode)
                 assert np.array_equal(bits(fn(a, w, n, k, bias, 0, n, None, gelu)), bits(ref))
+        wd = rng.normal(0, 0.1, (n, k)).astype(np.float32)
+        for gelu in (False, True):
+            assert np.array_equal(bits(O.gemm_dense(a, wd, bias, gelu)), bits(O.ref_gemm_dense(a, wd, bias, gelu=gelu)))
         qa, sa, qs = O.quantize_act(a)
         rqa, rsa, rqs = O.ref_quantize_activations(a)
         assert np.array_equal(qa, rqa) and np.array_equal(bits(sa), bits(rsa)) and np.array_equal(qs, rqs)
