@@ -98,12 +98,14 @@ __device__ __forceinline__ uint2 dequant4(uint32_t word, float d) {
 // Direct global -> LDS loads (16 or 4 bytes per lane): lane i's bytes from base + off land at LDS address lds + 16 i
 // (4 i). Written as inline assembly so that the compiler, which cannot tell which LDS bytes such a load writes, does
 // not wait for every one of them before each LDS access; the kernel's explicit vmcnt waits and barriers order them.
-// base and lds are wave-uniform; one wait state separates the M0 write from the load.
+// base and lds are wave-uniform. The compiler does not see the vector-memory instruction inside the assembly, so
+// the assembly supplies the wait states itself: five, enough for an M0 or SGPR operand written just before by a
+// scalar or vector instruction (a vector write of an SGPR read by a vector-memory instruction needs five).
 __device__ __forceinline__ void lds_dma16(const char* base, uint32_t off, uint32_t lds) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+    asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
 }
 __device__ __forceinline__ void lds_dma4(const char* base, uint32_t off, uint32_t lds) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+    asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
 }
 
 // s_waitcnt on the vector-memory counter only (expcnt and lgkmcnt left at their maximum).
@@ -182,7 +184,8 @@ __device__ __forceinline__ void epilogue_fast(const GemmParams& p, const f32x16 
     }
 }
 
-template <typename T, bool TILED>
+// SPLIT: the stream-K variant (sp.part set); a separate instantiation keeps its registers out of the whole-tile kernel
+template <typename T, bool TILED, bool SPLIT>
 __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, int vec4, PipeSplit sp) {
     typedef typename PipeMfma<T>::vec Vec;
     __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
@@ -198,7 +201,7 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
     const char* xg;  // activations / weight bytes of the segment's first stage
     const char* wg;
     int nsteps;      // stages in the segment
-    auto start_segment = [&](int m0, int n0, int k0, int n) {
+    auto start_segment = [&](int m0, int n0, int k0, int n) __attribute__((always_inline)) {
         const int r = tid >> 3, c = (tid & 7) ^ ((r >> 1) & 7);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -218,7 +221,7 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
     };
 
     const uint32_t lds0 = (uint32_t)(size_t)(lds_char*)smem;
-    auto issue_a = [&](int s) {
+    auto issue_a = [&](int s) __attribute__((always_inline)) {
         const char* base = xg + (size_t)s * 128;
         const uint32_t dst = lds0 + (s % 3) * kABuf + wave * 1024;
 #pragma unroll
@@ -229,10 +232,10 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
     const uint32_t w_dst4 = wave < (kRawUnits - 2048) / 64 ? kRawBase + 4 * 2048 + wave * 256 : kJunk;
     // tiled weights: the stage's 8704 bytes are contiguous: 16 bytes per lane, 1 KB per wave, and the last 512 bytes
     // by the first half of wave 0
-    auto issue_w_tiled_rest = [&](const char* base, int slot) {
+    auto issue_w_tiled_rest = [&](const char* base, int slot) __attribute__((always_inline)) {
         if (wave == 0 && lane < 32) lds_dma16(base, (uint32_t)(8192 + lane * 16), lds0 + kRawBase + slot * kRawBuf + 8192);
     };
-    auto issue_w = [&](int s) {
+    auto issue_w = [&](int s) __attribute__((always_inline)) {
         if (TILED) {
             const char* base = wg + (size_t)s * kRawBuf;
             lds_dma16(base, (uint32_t)(tid * 16), lds0 + kRawBase + (s % 3) * kRawBuf + wave * 1024);
@@ -253,11 +256,11 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
     struct RawIn {
         uint32_t w0, w8, a0, a1, a2, b0, b1;
     };
-    auto convert_load = [&](int s) {
+    auto convert_load = [&](int s) __attribute__((always_inline)) {
         const uint32_t* rw = reinterpret_cast<const uint32_t*>(smem + kRawBase + (s % 3) * kRawBuf + cv_row * 68);
         return RawIn{rw[0], rw[8], rw[2 * cv_q], rw[2 * cv_q + 1], rw[2 * cv_q + 2], rw[9 + 2 * cv_q], rw[10 + 2 * cv_q]};
     };
-    auto convert_store = [&](int s, const RawIn& r) {
+    auto convert_store = [&](int s, const RawIn& r) __attribute__((always_inline)) {
         const float d0 = half_bits_to_float((uint16_t)(r.w0 & 0xffff));
         const float d1 = half_bits_to_float((uint16_t)(r.w8 >> 16));
         // block 0's codes start at byte 2 of the row (two bytes off dword alignment), block 1's at byte 36
@@ -266,7 +269,7 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
         *reinterpret_cast<uint4*>(bdst) = dequant8<T>(c0, d0);
         *reinterpret_cast<uint4*>(bdst + 64) = dequant8<T>(make_uint2(r.b0, r.b1), d1);
     };
-    auto convert = [&](int s) { convert_store(s, convert_load(s)); };
+    auto convert = [&](int s) __attribute__((always_inline)) { convert_store(s, convert_load(s)); };
 
     // ---- MFMA operand addresses (bytes within a buffer)
     // weights (MFMA rows): output column wn*64 + tn*32 + lane%32, k = 32 blk + 16 h + 8 (lane/32) + e
@@ -286,7 +289,7 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
 
     // MFMA operands of one stage in registers, in four groups g = 2 blk + h (16 deep each): w[g][tn], x[g][tm]
     Vec ow[4][2], ox[4][2];
-    auto read_group = [&](int s, int g) {
+    auto read_group = [&](int s, int g) __attribute__((always_inline)) {
         const char* ab = smem + (s % 3) * kABuf;
         const char* bb = smem + kBBase + (s & 1) * kBBuf + b_lane;
         const int blk = g >> 1, h = g & 1;
@@ -296,18 +299,18 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
             ox[g][t] = *reinterpret_cast<const Vec*>(ab + x_lane[blk][h] + t * 32 * 128);
         }
     };
-    auto read_operands = [&](int s) {
+    auto read_operands = [&](int s) __attribute__((always_inline)) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) read_group(s, g);
     };
-    auto mfma_group = [&](int g) {
+    auto mfma_group = [&](int g) __attribute__((always_inline)) {
 #pragma unroll
         for (int tm = 0; tm < 2; ++tm)
 #pragma unroll
             for (int tn = 0; tn < 2; ++tn) acc[tm][tn] = PipeMfma<T>::run(ow[g][tn], ox[g][tm], acc[tm][tn]);
     };
 
-    auto run_segment = [&]() {
+    auto run_segment = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -341,7 +344,7 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
     // Steady stages (s + 4 < nsteps) are one basic block, scheduled so that the MFMAs are spread over the stage
     // with the LDS reads and the conversion arithmetic issued between them (the matrix core runs an MFMA while the
     // wave issues the following independent instructions).
-    auto stage_steady = [&](int s) {
+    auto stage_steady = [&](int s) __attribute__((always_inline)) {
         const RawIn raw = convert_load(s + 2);
         __builtin_amdgcn_sched_barrier(0);
         // four segments, one per operand group: a quarter of the global loads (one activation load, one or two
@@ -396,7 +399,7 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
             wait_vm<9>();
         __syncthreads();
     };
-    auto stage_tail = [&](int s) {
+    auto stage_tail = [&](int s) __attribute__((always_inline)) {
         if (s + 3 < nsteps) issue_a(s + 3);
         if (s + 2 < nsteps) convert(s + 2);
 #pragma unroll
@@ -417,7 +420,7 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
     };
 
     // ---- epilogue from the registers
-    auto epilogue = [&](int m0, int n0) {
+    auto epilogue = [&](int m0, int n0) __attribute__((always_inline)) {
     const int row0 = m0 + wm * 64 + (lane & 31);
     const int col0 = n0 + wn * 64 + 4 * (lane >> 5);
     constexpr int kYdt = std::is_same<T, __bf16>::value ? IDOLQ_BF16 : IDOLQ_F16;
@@ -447,14 +450,14 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
     int r = blockIdx.x;
     if (sp.G % 8 == 0) r = (r % 8) * (sp.G / 8) + r / 8;  // ranges on one XCD are consecutive
     const int ntiles = p.tiles_m * p.tiles_n;
-    auto tile_at = [&](int t, int& m0, int& n0) {
+    auto tile_at = [&](int t, int& m0, int& n0) __attribute__((always_inline)) {
         constexpr int G8 = 8;  // groups of 8 row-tiles, walked column by column
         const int per_group = G8 * p.tiles_n, group = t / per_group, first = group * G8;
         const int gm = min(p.tiles_m - first, G8), in_group = t - group * per_group;
         m0 = (first + in_group % gm) * kPipeBM;
         n0 = (in_group / gm) * kPipeBN;
     };
-    if (sp.part == nullptr) {
+    if constexpr (!SPLIT) {
         for (int t = r; t < ntiles; t += sp.G) {
             int m0, n0;
             tile_at(t, m0, n0);
@@ -464,11 +467,11 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
             __syncthreads();
         }
         return;
-    }
+    } else {
     const int64_t begin = (int64_t)r * sp.L + min(r, sp.R);
     const int64_t end = begin + sp.L + (r < sp.R ? 1 : 0);
     // range holding global stage index i
-    auto owner = [&](int64_t i) {
+    auto owner = [&](int64_t i) __attribute__((always_inline)) {
         const int64_t big = (int64_t)sp.R * (sp.L + 1);
         return (int)(i < big ? i / (sp.L + 1) : sp.R + (i - big) / sp.L);
     };
@@ -530,6 +533,7 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
         }
         __syncthreads();
         i += n;
+    }
     }
 }
 
@@ -596,10 +600,10 @@ int launch_pipe(GemmParams p, int xt, void* workspace, size_t workspace_bytes, h
         sp.G = tiles < cus ? tiles : cus;
     }
     const dim3 grid(sp.G), block(kThreads);
-    void* fn = xt == XT_BF16 ? (p.w_tiled ? reinterpret_cast<void*>(&q8_gemm_pipe_kernel<__bf16, true>)
-                                          : reinterpret_cast<void*>(&q8_gemm_pipe_kernel<__bf16, false>))
-                             : (p.w_tiled ? reinterpret_cast<void*>(&q8_gemm_pipe_kernel<_Float16, true>)
-                                          : reinterpret_cast<void*>(&q8_gemm_pipe_kernel<_Float16, false>));
+    void* fn = xt == XT_BF16 ? (p.w_tiled ? reinterpret_cast<void*>(&q8_gemm_pipe_kernel<__bf16, true, true>)
+                                          : reinterpret_cast<void*>(&q8_gemm_pipe_kernel<__bf16, false, true>))
+                             : (p.w_tiled ? reinterpret_cast<void*>(&q8_gemm_pipe_kernel<_Float16, true, true>)
+                                          : reinterpret_cast<void*>(&q8_gemm_pipe_kernel<_Float16, false, true>));
     if (split) {
         // a workgroup may wait for a later one: all must be resident at once
         void* args[] = {&p, &vec4, &sp};
@@ -607,7 +611,8 @@ int launch_pipe(GemmParams p, int xt, void* workspace, size_t workspace_bytes, h
         if (e != hipSuccess) return fail(IDOLQ_ELAUNCH, std::string("q8_gemm_pipe_kernel: ") + hipGetErrorString(e));
         return check_launch("q8_gemm_pipe_kernel");
     }
-#define IDOLQ_LAUNCH_PIPE(TT, TILED) hipLaunchKernelGGL((q8_gemm_pipe_kernel<TT, TILED>), grid, block, 0, stream, p, vec4, sp)
+#define IDOLQ_LAUNCH_PIPE(TT, TILED) \
+    hipLaunchKernelGGL((q8_gemm_pipe_kernel<TT, TILED, false>), grid, block, 0, stream, p, vec4, sp)
     if (xt == XT_BF16) {
         if (p.w_tiled) IDOLQ_LAUNCH_PIPE(__bf16, true); else IDOLQ_LAUNCH_PIPE(__bf16, false);
     } else {
