@@ -101,6 +101,13 @@ __device__ __forceinline__ uint2 dequant4(uint32_t word, float d) {
 // base and lds are wave-uniform. The compiler does not see the vector-memory instruction inside the assembly, so
 // the assembly supplies the wait states itself: five, enough for an M0 or SGPR operand written just before by a
 // scalar or vector instruction (a vector write of an SGPR read by a vector-memory instruction needs five).
+// A wave-uniform pointer in scalar registers (the value must be the same in every lane).
+__device__ __forceinline__ const char* uniform_ptr(const char* ptr) {
+    const uint64_t v = reinterpret_cast<uint64_t>(ptr);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<const char*>(((uint64_t)hi << 32) | lo);
+}
+
 __device__ __forceinline__ void lds_dma16(const char* base, uint32_t off, uint32_t lds) {
     asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
 }
@@ -132,30 +139,37 @@ __device__ __forceinline__ float act_fast(float v) {
 }
 
 // The common epilogue: y and the residual (if any) of the activation dtype T, fp32 bias (if any), n a multiple of 4
-// and 4-element groups vector-aligned. All loads are issued before the first store: a wait for a load also waits for every store issued
-// before it.
-template <typename T, int ACT>
-__device__ __forceinline__ void epilogue_fast(const GemmParams& p, const f32x16 (&acc)[2][2], int row0, int col0) {
-    typedef typename PipeMfma<T>::pair T2;
-    const bool round_first = (p.flags & IDOLQ_FLAG_ROUND_BEFORE_BIAS) != 0;
+// and 4-element groups vector-aligned. All loads are issued (epilogue_loads) before the first store
+// (epilogue_stores): a wait for a load also waits for every store issued before it.
+struct EpilogueLoads {
     float4 b4[2][4];
     uint2 r2[2][2][4];
+};
+
+__device__ __forceinline__ void epilogue_loads(const GemmParams& p, int row0, int col0, EpilogueLoads& L) {
 #pragma unroll
     for (int tn = 0; tn < 2; ++tn)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int col = col0 + tn * 32 + 8 * g;
             const bool full = col < p.n;
-            b4[tn][g] = p.bias && full ? *reinterpret_cast<const float4*>(static_cast<const float*>(p.bias) + col)
-                                       : make_float4(0, 0, 0, 0);
+            L.b4[tn][g] = p.bias && full ? *reinterpret_cast<const float4*>(static_cast<const float*>(p.bias) + col)
+                                         : make_float4(0, 0, 0, 0);
 #pragma unroll
             for (int tm = 0; tm < 2; ++tm) {
                 const int row = row0 + tm * 32;
-                r2[tm][tn][g] = p.res && full && row < p.m
-                                    ? *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.res) + (int64_t)row * p.ldr + col)
-                                    : make_uint2(0, 0);
+                L.r2[tm][tn][g] = p.res && full && row < p.m
+                                      ? *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.res) + (int64_t)row * p.ldr + col)
+                                      : make_uint2(0, 0);
             }
         }
+}
+
+template <typename T, int ACT>
+__device__ __forceinline__ void epilogue_stores(const GemmParams& p, const f32x16 (&acc)[2][2], int row0, int col0,
+                                                const EpilogueLoads& L) {
+    typedef typename PipeMfma<T>::pair T2;
+    const bool round_first = (p.flags & IDOLQ_FLAG_ROUND_BEFORE_BIAS) != 0;
 #pragma unroll
     for (int tm = 0; tm < 2; ++tm) {
         const int row = row0 + tm * 32;
@@ -171,8 +185,8 @@ __device__ __forceinline__ void epilogue_fast(const GemmParams& p, const f32x16 
                     lo = __builtin_convertvector(__builtin_convertvector(lo, T2), f32x2);
                     hi = __builtin_convertvector(__builtin_convertvector(hi, T2), f32x2);
                 }
-                const float4 b = b4[tn][g];
-                const T2 rlo = __builtin_bit_cast(T2, r2[tm][tn][g].x), rhi = __builtin_bit_cast(T2, r2[tm][tn][g].y);
+                const float4 b = L.b4[tn][g];
+                const T2 rlo = __builtin_bit_cast(T2, L.r2[tm][tn][g].x), rhi = __builtin_bit_cast(T2, L.r2[tm][tn][g].y);
                 lo = lo + f32x2{b.x, b.y} + __builtin_convertvector(rlo, f32x2);
                 hi = hi + f32x2{b.z, b.w} + __builtin_convertvector(rhi, f32x2);
                 lo = f32x2{act_fast<ACT>(lo.x), act_fast<ACT>(lo.y)};
@@ -184,7 +198,6 @@ __device__ __forceinline__ void epilogue_fast(const GemmParams& p, const f32x16 
     }
 }
 
-// SPLIT: the stream-K variant (sp.part set); a separate instantiation keeps its registers out of the whole-tile kernel
 template <typename T, bool TILED, bool SPLIT>
 __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, int vec4, PipeSplit sp) {
     typedef typename PipeMfma<T>::vec Vec;
@@ -214,9 +227,9 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
             const int row = min(n0 + u / 17, p.n - 1);
             w_off[j] = (uint32_t)((int64_t)row * p.row_bytes + (u % 17) * 4);
         }
-        xg = static_cast<const char*>(p.x) + (size_t)k0 * 128;
-        wg = TILED ? reinterpret_cast<const char*>(p.w) + ((size_t)(n0 / kPipeBN) * (p.k / 64) + k0) * kRawBuf
-                   : reinterpret_cast<const char*>(p.w) + (size_t)k0 * 68;
+        xg = uniform_ptr(static_cast<const char*>(p.x) + (size_t)k0 * 128);
+        wg = uniform_ptr(TILED ? reinterpret_cast<const char*>(p.w) + ((size_t)(n0 / kPipeBN) * (p.k / 64) + k0) * kRawBuf
+                               : reinterpret_cast<const char*>(p.w) + (size_t)k0 * 68);
         nsteps = n;
     };
 
@@ -310,6 +323,15 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
             for (int tn = 0; tn < 2; ++tn) acc[tm][tn] = PipeMfma<T>::run(ow[g][tn], ox[g][tm], acc[tm][tn]);
     };
 
+    // the segment's first loads: activations 0 and 1, weight bytes 0..2 (LDS must no longer be read by the previous
+    // segment)
+    auto prologue_issue = [&]() __attribute__((always_inline)) {
+        issue_a(0);
+        issue_w(0);
+        if (nsteps > 1) issue_w(1);
+        if (nsteps > 1) issue_a(1);
+        if (nsteps > 2) issue_w(2);
+    };
     auto run_segment = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -318,14 +340,9 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    // ---- prologue. At the start of stage s, stage s's operands are in registers, activations s + 1 and weights
-    // s + 1 (converted) are in LDS, weight bytes s + 2 have landed, activations s + 2 and weight bytes s + 3 are in
-    // flight.
-    issue_a(0);
-    issue_w(0);
-    if (nsteps > 1) issue_w(1);
-    if (nsteps > 1) issue_a(1);
-    if (nsteps > 2) issue_w(2);
+    // ---- prologue (its first loads were issued by prologue_issue). At the start of stage s, stage s's operands are
+    // in registers, activations s + 1 and weights s + 1 (converted) are in LDS, weight bytes s + 2 have landed,
+    // activations s + 2 and weight bytes s + 3 are in flight.
     wait_vm<0>();
     __syncthreads();
     convert(0);
@@ -420,14 +437,23 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
     };
 
     // ---- epilogue from the registers
+    constexpr int kYdt = std::is_same<T, __bf16>::value ? IDOLQ_BF16 : IDOLQ_F16;
+    // the register epilogue applies (the same for every tile of the launch)
+    const bool fast_epilogue = vec4 && p.n % 4 == 0 && p.y_dt == kYdt && (!p.res || p.res_dt == kYdt) &&
+                               (!p.bias || p.bias_dt == IDOLQ_F32) &&
+                               (p.act == IDOLQ_ACT_NONE || p.act == IDOLQ_ACT_GELU_TANH || p.act == IDOLQ_ACT_RELU);
+    auto fast_stores = [&](int row0, int col0, const EpilogueLoads& L) __attribute__((always_inline)) {
+        if (p.act == IDOLQ_ACT_NONE) return epilogue_stores<T, IDOLQ_ACT_NONE>(p, acc, row0, col0, L);
+        if (p.act == IDOLQ_ACT_GELU_TANH) return epilogue_stores<T, IDOLQ_ACT_GELU_TANH>(p, acc, row0, col0, L);
+        return epilogue_stores<T, IDOLQ_ACT_RELU>(p, acc, row0, col0, L);
+    };
     auto epilogue = [&](int m0, int n0) __attribute__((always_inline)) {
     const int row0 = m0 + wm * 64 + (lane & 31);
     const int col0 = n0 + wn * 64 + 4 * (lane >> 5);
-    constexpr int kYdt = std::is_same<T, __bf16>::value ? IDOLQ_BF16 : IDOLQ_F16;
-    if (vec4 && p.n % 4 == 0 && p.y_dt == kYdt && (!p.res || p.res_dt == kYdt) && (!p.bias || p.bias_dt == IDOLQ_F32)) {
-        if (p.act == IDOLQ_ACT_NONE) return epilogue_fast<T, IDOLQ_ACT_NONE>(p, acc, row0, col0);
-        if (p.act == IDOLQ_ACT_GELU_TANH) return epilogue_fast<T, IDOLQ_ACT_GELU_TANH>(p, acc, row0, col0);
-        if (p.act == IDOLQ_ACT_RELU) return epilogue_fast<T, IDOLQ_ACT_RELU>(p, acc, row0, col0);
+    if (fast_epilogue) {
+        EpilogueLoads L;
+        epilogue_loads(p, row0, col0, L);
+        return fast_stores(row0, col0, L);
     }
     // General path: the accumulators go to LDS (element i of thread t at float i * 512 + t; LDS is no longer read by
     // the main loop after its last barrier) and one loop that is not unrolled runs them through the epilogue.
@@ -454,17 +480,44 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
         constexpr int G8 = 8;  // groups of 8 row-tiles, walked column by column
         const int per_group = G8 * p.tiles_n, group = t / per_group, first = group * G8;
         const int gm = min(p.tiles_m - first, G8), in_group = t - group * per_group;
-        m0 = (first + in_group % gm) * kPipeBM;
-        n0 = (in_group / gm) * kPipeBN;
+        // integer division runs on the vector unit: bring the (uniform) results back to scalar registers
+        m0 = __builtin_amdgcn_readfirstlane((first + in_group % gm) * kPipeBM);
+        n0 = __builtin_amdgcn_readfirstlane((in_group / gm) * kPipeBN);
     };
     if constexpr (!SPLIT) {
-        for (int t = r; t < ntiles; t += sp.G) {
-            int m0, n0;
-            tile_at(t, m0, n0);
+        // With the register epilogue, the next tile's first loads are issued between the epilogue's loads and its
+        // arithmetic and stores, which hide their latency (the epilogue does not use LDS).
+        int m0 = 0, n0 = 0;
+        if (r < ntiles) {
+            tile_at(r, m0, n0);
             start_segment(m0, n0, 0, sp.S);
+            prologue_issue();
+        }
+        for (int t = r; t < ntiles; t += sp.G) {
             run_segment();
-            epilogue(m0, n0);
-            __syncthreads();
+            const int tn = t + sp.G, cm0 = m0, cn0 = n0;
+            if (fast_epilogue) {
+                const int row0 = cm0 + wm * 64 + (lane & 31), col0 = cn0 + wn * 64 + 4 * (lane >> 5);
+                EpilogueLoads L;
+                epilogue_loads(p, row0, col0, L);
+                // the epilogue's loads complete first: a compiler wait for one of them would otherwise also wait for
+                // the later loads issued below, which it cannot see
+                wait_vm<0>();
+                if (tn < ntiles) {
+                    tile_at(tn, m0, n0);
+                    start_segment(m0, n0, 0, sp.S);
+                    prologue_issue();
+                }
+                fast_stores(row0, col0, L);
+            } else {
+                epilogue(cm0, cn0);
+                __syncthreads();
+                if (tn < ntiles) {
+                    tile_at(tn, m0, n0);
+                    start_segment(m0, n0, 0, sp.S);
+                    prologue_issue();
+                }
+            }
         }
         return;
     } else {
@@ -487,6 +540,7 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
         int m0, n0;
         tile_at(t, m0, n0);
         start_segment(m0, n0, k0, n);
+        prologue_issue();
         run_segment();
         if (k0 > 0) {
             // a later part of the tile: store the partial accumulators (pair q of thread tid at q * 512 + tid), wait
