@@ -52,11 +52,9 @@ struct AttnMfma<_Float16> {
     }
 };
 
-template <typename T>
-__device__ __forceinline__ _Float16 to_half(uint16_t bits) {
-    if (std::is_same<T, _Float16>::value) return __builtin_bit_cast(_Float16, bits);
-    return static_cast<_Float16>(bf16_bits_to_float(bits));
-}
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
 
 template <typename T>
 __global__ __launch_bounds__(256) void attn_mfma_hd64(AttnParams p) {
@@ -88,26 +86,48 @@ __global__ __launch_bounds__(256) void attn_mfma_hd64(AttnParams p) {
     for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[t][r] = 0.0f;
-    float m_run = -INFINITY, l_run = 0.0f;
 
-    for (int64_t j0 = 0; j0 < p.lk; j0 += kBKV) {
+    // The running maximum mc is kept in the scaled (base-2) domain and raised lazily: only when a tile's scores
+    // exceed it by more than 8, so probabilities stay below 2^8 (well inside fp16) and most tiles skip the
+    // rescaling of o and l. Scores are turned into u = s * c - mc first (the maximum is taken over u: products of
+    // an FMA need no NaN canonicalization, MFMA results would). l is summed per lane (half of each query's keys)
+    // and combined at the end.
+    const float c = p.scale_log2;
+    float mc = -INFINITY, l_part = 0.0f;
+    const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+
+    // one 64-key tile; MASK: the last tile, which holds fewer than 64 keys; FIRST: the first tile, which sets mc
+    auto tile = [&](int64_t j0, auto mask_tag, auto first_tag) __attribute__((always_inline)) {
+        constexpr bool MASK = decltype(mask_tag)::value, FIRST = decltype(first_tag)::value;
         __syncthreads();
-        // Stage K [key][d] and V^T [d][key]: 512 sixteen-byte units each, 2 per thread.
+        // Stage K [key][d] and V^T [d][key] (fp16): thread t takes keys 2 (t / 8) and 2 (t / 8) + 1, d chunk
+        // 8 (t % 8); V^T gets one (key, key + 1) pair per d and dword store.
+        {
+            const int kp = threadIdx.x >> 3, part = threadIdx.x & 7;
+            uint4 kr[2], vr[2];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int u = threadIdx.x + i * 256;
-            const int key = u >> 3, part = u & 7;
-            uint4 kr = make_uint4(0, 0, 0, 0), vr = make_uint4(0, 0, 0, 0);
-            if (j0 + key < p.lk) {
-                kr = *reinterpret_cast<const uint4*>(kbase + (j0 + key) * p.ldkv + 8 * part);
-                vr = *reinterpret_cast<const uint4*>(vbase + (j0 + key) * p.ldkv + 8 * part);
+            for (int i = 0; i < 2; ++i) {
+                const int64_t key = j0 + 2 * kp + i;
+                kr[i] = make_uint4(0, 0, 0, 0);
+                vr[i] = make_uint4(0, 0, 0, 0);
+                if (key < p.lk) {
+                    kr[i] = *reinterpret_cast<const uint4*>(kbase + key * p.ldkv + 8 * part);
+                    vr[i] = *reinterpret_cast<const uint4*>(vbase + key * p.ldkv + 8 * part);
+                }
+                *reinterpret_cast<uint4*>(k_lds + (2 * kp + i) * kKPitch + 8 * part) = kr[i];
             }
-            *reinterpret_cast<uint4*>(k_lds + key * kKPitch + 8 * part) = kr;
-            const uint32_t vw[4] = {vr.x, vr.y, vr.z, vr.w};
+            const uint32_t v0[4] = {vr[0].x, vr[0].y, vr[0].z, vr[0].w}, v1[4] = {vr[1].x, vr[1].y, vr[1].z, vr[1].w};
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const uint16_t bits = (uint16_t)(vw[e >> 1] >> (16 * (e & 1)));
-                vt_lds[(8 * part + e) * kVPitch + key] = __builtin_bit_cast(uint16_t, to_half<T>(bits));
+                const uint16_t b0 = (uint16_t)(v0[e >> 1] >> (16 * (e & 1))), b1 = (uint16_t)(v1[e >> 1] >> (16 * (e & 1)));
+                f16x2 pair;
+                if (std::is_same<T, _Float16>::value) {
+                    pair = f16x2{__builtin_bit_cast(_Float16, b0), __builtin_bit_cast(_Float16, b1)};
+                } else {
+                    const f32x2 f = {bf16_bits_to_float(b0), bf16_bits_to_float(b1)};
+                    pair = __builtin_convertvector(f, f16x2);
+                }
+                *reinterpret_cast<f16x2*>(vt_lds + (8 * part + e) * kVPitch + 2 * kp) = pair;
             }
         }
         __syncthreads();
@@ -117,43 +137,48 @@ __global__ __launch_bounds__(256) void attn_mfma_hd64(AttnParams p) {
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) s[st][r] = 0.0f;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const Vec a = *reinterpret_cast<const Vec*>(k_lds + (st * 32 + (lane & 31)) * kKPitch + 16 * c + 8 * half);
-                s[st] = AttnMfma<T>::run(a, qf[c], s[st]);
+            for (int c4 = 0; c4 < 4; ++c4) {
+                const Vec a = *reinterpret_cast<const Vec*>(k_lds + (st * 32 + (lane & 31)) * kKPitch + 16 * c4 + 8 * half);
+                s[st] = AttnMfma<T>::run(a, qf[c4], c4 == 0 ? f32x16{} : s[st]);
             }
         }
-        // Online softmax for query qi over the 64 keys (32 here, 32 in lane ^ 32).
-        float mx = -INFINITY;
+        if (MASK) {
+            // keys past lk get no weight
+            const int valid = (int)(p.lk - j0);
 #pragma unroll
-        for (int st = 0; st < 2; ++st)
+            for (int st = 0; st < 2; ++st)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t key = j0 + st * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                const float t = key < p.lk ? s[st][r] * p.scale_log2 : -INFINITY;
-                s[st][r] = t;
-                mx = fmaxf(mx, t);
+                for (int r = 0; r < 16; ++r)
+                    if (st * 32 + 8 * (r >> 2) + 4 * half + (r & 3) >= valid) s[st][r] = -INFINITY;
+        }
+        if (FIRST) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) mx = fmaxf(mx, s[i >> 4][i & 15]);
+            mc = fmaxf(mx, __shfl_xor(mx, 32)) * c;
+        }
+#pragma unroll
+        for (int i = 0; i < 32; ++i) s[i >> 4][i & 15] = fmaf(s[i >> 4][i & 15], c, -mc);
+        if (!FIRST) {
+            // maximum over this lane's 32 values, then over the query's other 32 (lane ^ 32)
+            float mx = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 32; i += 2) mx = fmaxf(mx, fmaxf(s[i >> 4][i & 15], s[i >> 4][(i & 15) + 1]));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const bool raise = mx > 8.0f;
+            if (__builtin_amdgcn_ballot_w64(raise) != 0) {  // a wave-uniform branch: most tiles skip it
+                const float delta = raise ? mx : 0.0f;
+                const float alpha = __builtin_amdgcn_exp2f(-delta);
+                l_part *= alpha;
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+#pragma unroll
+                for (int i = 0; i < 32; ++i) s[i >> 4][i & 15] -= delta;
+                mc += delta;
             }
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = exp2f(m_run - m_new);
-        float lsum = 0.0f;
-#pragma unroll
-        for (int st = 0; st < 2; ++st)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float e = exp2f(s[st][r] - m_new);
-                s[st][r] = e;
-                lsum += e;
-            }
-        lsum += __shfl_xor(lsum, 32);
-        l_run = l_run * alpha + lsum;
-        m_run = m_new;
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+        }
 
         // O^T += V^T * P^T over 4 chunks of 16 keys. Chunk (st, kc) uses accumulator elements r = 8 kc + e of
         // sub-tile st; slot 8 * half + e of the MFMA's k holds key st*32 + 16 kc + 8 (e / 4) + 4 half + e % 4.
@@ -163,7 +188,15 @@ __global__ __launch_bounds__(256) void attn_mfma_hd64(AttnParams p) {
             for (int kc = 0; kc < 2; ++kc) {
                 f16x8 pf;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) pf[e] = static_cast<_Float16>(s[st][8 * kc + e]);
+                for (int e = 0; e < 8; e += 2) {
+                    const f32x2 pe = {__builtin_amdgcn_exp2f(s[st][8 * kc + e]),
+                                      __builtin_amdgcn_exp2f(s[st][8 * kc + e + 1])};
+                    const f16x2 h = __builtin_convertvector(pe, f16x2);
+                    pf[e] = h.x;
+                    pf[e + 1] = h.y;
+                    // the normalizer sums the probabilities as rounded for the product
+                    l_part = __builtin_amdgcn_fdot2(h, ones, l_part, false);
+                }
                 const int key0 = st * 32 + 16 * kc + 4 * half;
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
@@ -174,8 +207,17 @@ __global__ __launch_bounds__(256) void attn_mfma_hd64(AttnParams p) {
                     o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pf, o[t], 0, 0, 0);
                 }
             }
+    };
+    const int64_t full_end = p.lk / kBKV * kBKV;
+    if (full_end == 0) {
+        tile(0, std::true_type{}, std::true_type{});
+    } else {
+        tile(0, std::false_type{}, std::true_type{});
+        for (int64_t j0 = kBKV; j0 < full_end; j0 += kBKV) tile(j0, std::false_type{}, std::false_type{});
+        if (full_end < p.lk) tile(full_end, std::true_type{}, std::false_type{});
     }
 
+    const float l_run = l_part + __shfl_xor(l_part, 32);
     if (qi >= p.lq) return;
     const float inv = 1.0f / l_run;
     const int64_t obase = b * p.o_bs + qi * p.ldo + h * kHD;
