@@ -4,9 +4,11 @@
 // one (batch, head); each wave owns 32 queries. Key/value tiles of 64 rows are staged in LDS (K as [key][d],
 // V transposed to [d][key] in fp16) and shared by the 4 waves. Scores are computed transposed, S^T = K * Q^T, so a
 // lane holds 32 scores of a single query (its column) and the online softmax (fp32, base-2 exponent with the
-// 1/sqrt(64) * log2(e) factor folded in) needs one cross-lane exchange (lanes l and l + 32). The probabilities stay in
-// registers and become, converted to fp16, the B operand of O^T = V^T * P^T; the MFMA's k order is permuted to the
-// order in which the score accumulator holds the keys, and the V^T operand is read in that same order.
+// 1/sqrt(64) * log2(e) factor folded in) needs one cross-lane exchange (lanes l and l + 32). The running maximum is
+// raised only when a tile exceeds it by more than 2^8 in probability, so most tiles skip rescaling. The probabilities
+// stay in registers and become, converted to fp16, the B operand of O^T = V^T * P^T (the row sums are taken from the
+// same fp16 values with dot2); the MFMA's k order is permuted to the order in which the score accumulator holds the
+// keys, and the V^T operand is read in that same order.
 //
 // attn_f32 (any dtype, head_dim <= 256): one wave per (query, head, batch), 64 keys per step with one key per lane
 // for the scores and the head dimension split over lanes for P * V; fp32 throughout. Used for fp32 activations
