@@ -51,6 +51,30 @@ def test_adaln_batches_in_place_and_bf16():
     assert np.max(np.abs(L.layernorm(to_dev(x2), 1e-6).cpu().numpy() - O.norm_rows(x2, 1e-6))) < 1e-5
 
 
+@pytest.mark.parametrize("dtype,dim", [(torch.bfloat16, 1536), (torch.float16, 1024), (torch.float32, 1536),
+                                       (torch.bfloat16, 512), (torch.bfloat16, 4096)])
+def test_vector_rows_match_the_general_kernel(dtype, dim):
+    # aligned rows take the one-wave-per-row kernel, a view with an odd row stride the general one: same arithmetic
+    # (fp32 values, fp64 sums), so the results agree bit for bit, also in place and with adaLN per batch
+    rng = np.random.default_rng(dim)
+    rows = 2 * 515
+    x = torch.from_numpy(rng.normal(0.1, 1.3, (rows, dim)).astype(np.float32)).to(DEV).to(dtype)
+    wide = torch.zeros((rows, dim + 1), device=DEV, dtype=dtype)
+    wide[:, :dim] = x
+    odd = wide[:, :dim]
+    sh = to_dev(rng.normal(0, 0.1, (2, dim)).astype(np.float32))
+    sc = to_dev(rng.normal(0, 0.1, (2, dim)).astype(np.float32))
+    g = to_dev(rng.normal(1, 0.1, dim).astype(np.float32))
+    b = to_dev(rng.normal(0, 0.1, dim).astype(np.float32))
+    for kw in (dict(), dict(gamma=g, beta=b), dict(shift=sh, scale=sc, rows_per_batch=515)):
+        vec = L.layernorm(x, 1e-6, **kw)
+        gen = L.layernorm(odd, 1e-6, **kw)
+        assert torch.equal(vec, gen), kw
+    xi = x.clone()
+    L.layernorm(xi, 1e-6, shift=sh, scale=sc, rows_per_batch=515, out=xi)
+    assert torch.equal(xi, L.layernorm(odd, 1e-6, shift=sh, scale=sc, rows_per_batch=515))
+
+
 def test_attention_fp32_matches_reference_golden(golden):
     # the reference test shapes, strided rows (tests/test_kernels.cpp:184-228); fp32 kernel, 1e-5 norm-relative
     g = golden("attention")
