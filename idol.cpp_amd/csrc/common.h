@@ -58,6 +58,46 @@ __device__ __forceinline__ void store_from_float(void* p, int dt, int64_t i, flo
     }
 }
 
+// Eight consecutive elements of a dtype as fp32, through 16-byte accesses (the address must be 16-byte aligned).
+template <int DT>
+__device__ __forceinline__ void load8(const void* base, int64_t i, float (&f)[8]) {
+    if (DT == IDOLQ_F32) {
+        const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + i);
+        const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + i + 4);
+        f[0] = a.x, f[1] = a.y, f[2] = a.z, f[3] = a.w, f[4] = b.x, f[5] = b.y, f[6] = b.z, f[7] = b.w;
+    } else {
+        const uint4 r = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + i);
+        const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint16_t b = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+            f[e] = DT == IDOLQ_BF16 ? bf16_bits_to_float(b) : half_bits_to_float(b);
+        }
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void store8(void* base, int64_t i, const float (&f)[8]) {
+    if (DT == IDOLQ_F32) {
+        *reinterpret_cast<float4*>(static_cast<float*>(base) + i) = make_float4(f[0], f[1], f[2], f[3]);
+        *reinterpret_cast<float4*>(static_cast<float*>(base) + i + 4) = make_float4(f[4], f[5], f[6], f[7]);
+    } else {
+        uint32_t w[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint16_t lo = DT == IDOLQ_BF16 ? float_to_bf16_bits(f[2 * q]) : float_to_half_bits(f[2 * q]);
+            const uint16_t hi = DT == IDOLQ_BF16 ? float_to_bf16_bits(f[2 * q + 1]) : float_to_half_bits(f[2 * q + 1]);
+            w[q] = (uint32_t)lo | ((uint32_t)hi << 16);
+        }
+        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(base) + i) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+// The pointer and the row stride (elements of the dtype) allow 16-byte accesses to 8-element groups.
+inline bool vec8_ok(const void* p, int dt, int64_t ld) {
+    return reinterpret_cast<uintptr_t>(p) % 16 == 0 && (ld * (int64_t)dtype_size(dt)) % 16 == 0;
+}
+
 // Round a float through a dtype and back (identity for fp32).
 __device__ __forceinline__ float round_through(int dt, float v) {
     if (dt == IDOLQ_BF16) return bf16_bits_to_float(float_to_bf16_bits(v));

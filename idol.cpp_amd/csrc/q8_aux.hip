@@ -151,6 +151,44 @@ __global__ __launch_bounds__(256) void copy2d_kernel(const void* src, int sdt, i
     }
 }
 
+// 16-byte copies of 8-element groups: cols % 8 == 0 and both buffers vector-aligned.
+template <int SDT, int DDT>
+__global__ __launch_bounds__(256) void copy2d_vec_kernel(const void* src, int64_t lds, void* dst, int64_t ldd,
+                                                         int64_t rows, int64_t groups_per_row) {
+    const int64_t total = rows * groups_per_row, stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+        const int64_t r = i / groups_per_row, c = (i - r * groups_per_row) * 8;
+        float f[8];
+        load8<SDT>(src, r * lds + c, f);
+        store8<DDT>(dst, r * ldd + c, f);
+    }
+}
+
+// One thread per (row, coordinate): nfreq sines then nfreq cosines as 16-bit values, stored 8 at a time.
+template <int DT>
+__global__ __launch_bounds__(256) void pos_embed_vec_kernel(const float* __restrict__ coords, int64_t rows,
+                                                            const float* __restrict__ freqs, int nfreq, void* out,
+                                                            int64_t ldo) {
+    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= rows * 3) return;
+    const int64_t r = id / 3;
+    const int c = (int)(id - r * 3);
+    const float kPi = 3.14159265358979323846f;
+    const float v = coords[r * 3 + c];
+    const int64_t o = r * ldo + (int64_t)c * 2 * nfreq;
+    for (int j0 = 0; j0 < nfreq; j0 += 8) {
+        float sn[8], cs[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float ang = (v * freqs[j0 + e]) * kPi;
+            sn[e] = sinf(ang);
+            cs[e] = cosf(ang);
+        }
+        store8<DT>(out, o + j0, sn);
+        store8<DT>(out, o + nfreq + j0, cs);
+    }
+}
+
 unsigned grid_for(int64_t items, int threads = 256) {
     const int64_t g = (items + threads - 1) / threads;
     return (unsigned)(g < 1 ? 1 : g > 1048576 ? 1048576 : g);
@@ -260,6 +298,16 @@ extern "C" int idolq_pos_embed(const float* coords, int64_t rows, const float* f
     if (rows < 0 || nfreq <= 0 || nfreq > 65536 || ldo < 6 * nfreq) return fail(IDOLQ_EINVAL, "bad pos_embed shape");
     if (rows == 0) return IDOLQ_OK;
     if (!coords || !freqs || !out) return fail(IDOLQ_EINVAL, "coords, freqs and out must be non-null");
+    if (out_dtype != IDOLQ_F32 && nfreq % 8 == 0 && vec8_ok(out, out_dtype, ldo)) {
+        const unsigned blocks = (unsigned)((rows * 3 + 255) / 256);
+        if (out_dtype == IDOLQ_BF16)
+            hipLaunchKernelGGL(pos_embed_vec_kernel<IDOLQ_BF16>, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                               coords, rows, freqs, (int)nfreq, out, ldo);
+        else
+            hipLaunchKernelGGL(pos_embed_vec_kernel<IDOLQ_F16>, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                               coords, rows, freqs, (int)nfreq, out, ldo);
+        return check_launch("pos_embed_vec_kernel");
+    }
     const int64_t items = rows * 3 * nfreq;
     hipLaunchKernelGGL(pos_embed_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), coords, rows, freqs, (int)nfreq, out, out_dtype, ldo);
@@ -272,6 +320,22 @@ extern "C" int idolq_copy2d(const void* src, int src_dtype, int64_t lds, void* d
     if (rows < 0 || cols < 0 || lds < cols || ldd < cols) return fail(IDOLQ_EINVAL, "bad copy shape");
     if (rows * cols == 0) return IDOLQ_OK;
     if (!src || !dst) return fail(IDOLQ_EINVAL, "src and dst must be non-null");
+    if (cols % 8 == 0 && vec8_ok(src, src_dtype, lds) && vec8_ok(dst, dst_dtype, ldd)) {
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        const int64_t g = cols / 8;
+        const dim3 grid(grid_for(rows * g)), block(256);
+#define IDOLQ_COPY(S, D) hipLaunchKernelGGL((copy2d_vec_kernel<S, D>), grid, block, 0, s, src, lds, dst, ldd, rows, g)
+#define IDOLQ_COPY_TO(S)                                             \
+        if (dst_dtype == IDOLQ_F32) IDOLQ_COPY(S, IDOLQ_F32);        \
+        else if (dst_dtype == IDOLQ_BF16) IDOLQ_COPY(S, IDOLQ_BF16); \
+        else IDOLQ_COPY(S, IDOLQ_F16)
+        if (src_dtype == IDOLQ_F32) { IDOLQ_COPY_TO(IDOLQ_F32); }
+        else if (src_dtype == IDOLQ_BF16) { IDOLQ_COPY_TO(IDOLQ_BF16); }
+        else { IDOLQ_COPY_TO(IDOLQ_F16); }
+#undef IDOLQ_COPY_TO
+#undef IDOLQ_COPY
+        return check_launch("copy2d_vec_kernel");
+    }
     hipLaunchKernelGGL(copy2d_kernel, dim3(grid_for(rows * cols)), dim3(256), 0, static_cast<hipStream_t>(stream), src,
                        src_dtype, lds, dst, dst_dtype, ldd, rows, cols);
     return check_launch("copy2d_kernel");
