@@ -84,11 +84,11 @@ class MlpBlock:
 
     def up(self):
         self.L.gemm(self.x, self.w_up, H, bias=self.b_up, act=self.L.ACT_GELU_TANH, mode=self.mode, out=self.h,
-                    workspace=self.ws, tiled=self.tiled)
+                    workspace=self.ws, tiled=self.tiled, split=self.tiled)
 
     def down(self):
         self.L.gemm(self.h, self.w_down, D, bias=self.b_down, residual=self.x, mode=self.mode, out=self.y,
-                    workspace=self.ws, tiled=self.tiled)
+                    workspace=self.ws, tiled=self.tiled, split=self.tiled)
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "q8_gemm_mlp_block_traffic.md"
@@ -174,7 +174,7 @@ def run_gpu(args):
                      "frac": achieved / PEAK_TFLOPS[arith], "traffic": traffic["mean"] if traffic else None,
                      "traffic_per_launch": traffic,
                      "algorithmic_bytes": {"up": ALG_BYTES_UP, "down": ALG_BYTES_DOWN},
-                     "kernel": "q8_gemm_pipe_kernel" if args.mode == "dequant" else
+                     "kernel": "q8_wide_kernel" if args.mode == "dequant" else
                                "q8_gemm_kernel" if args.mode == "exact" else "q8_gemm_int8_kernel",
                      "launch_ms": {"up": up_ms, "down": down_ms},
                      "flop_per_launch": flop_gemm},

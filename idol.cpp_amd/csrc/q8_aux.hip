@@ -230,36 +230,51 @@ extern "C" int idolq_q8_0_dequant(const uint8_t* w, int64_t n, int64_t k, void* 
     return check_launch("q8_dequant_kernel");
 }
 
-// One dword of the tiled layout per thread: dword u of chunk (t, s) is dword u % 17 of stage s of row t * 128 + u / 17
-// (zero past the last row). Rows are 4-byte aligned since k % 64 == 0.
-__global__ __launch_bounds__(256) void q8_tile_kernel(const uint32_t* __restrict__ w, int64_t n, int64_t row_dwords,
-                                                      int stages, int64_t total, uint32_t* __restrict__ out) {
+// One dword of the grouped layout per thread. Dword u of chunk (g, s) (544 dwords):
+//   u < 512: byte 4 u of the codes: block b = u / 256, lane l = (u / 4) % 64, dword e = u % 4 of the lane's 16 bytes:
+//            codes 16 (e / 2) + 8 (l / 32) + 4 (e % 2) .. + 3 of block 2 s + b of row 32 g + l % 32;
+//   u >= 512: the two fp16 scales (blocks 2 s, 2 s + 1) of row 32 g + u - 512.
+// Rows past n are zero. A row's codes start 2 bytes into each 34-byte block, so they are read bytewise.
+__global__ __launch_bounds__(256) void q8_group_kernel(const uint8_t* __restrict__ w, int64_t n, int64_t row_bytes,
+                                                       int stages, int64_t total, uint32_t* __restrict__ out) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t chunk = i / 2176;
-        const int u = (int)(i - chunk * 2176);
-        const int64_t t = chunk / stages;
-        const int s = (int)(chunk - t * stages);
-        const int64_t row = t * 128 + u / 17;
-        out[i] = row < n ? w[row * row_dwords + (int64_t)s * 17 + u % 17] : 0u;
+        const int64_t chunk = i / 544;
+        const int u = (int)(i - chunk * 544);
+        const int64_t g = chunk / stages;
+        const int s = (int)(chunk - g * stages);
+        const int r = u < 512 ? ((u >> 2) & 63) & 31 : u - 512;
+        const int64_t row = g * 32 + r;
+        uint32_t v = 0;
+        if (row < n) {
+            const uint8_t* rp = w + row * row_bytes;
+            if (u < 512) {
+                const int b = u >> 8, l = (u >> 2) & 63, e = u & 3;
+                const uint8_t* q = rp + (int64_t)(2 * s + b) * kQ8Bytes + 2 + 16 * (e >> 1) + 8 * (l >> 5) + 4 * (e & 1);
+                v = (uint32_t)q[0] | ((uint32_t)q[1] << 8) | ((uint32_t)q[2] << 16) | ((uint32_t)q[3] << 24);
+            } else {
+                const uint8_t* d0 = rp + (int64_t)(2 * s) * kQ8Bytes;
+                v = (uint32_t)d0[0] | ((uint32_t)d0[1] << 8) | ((uint32_t)d0[kQ8Bytes] << 16) |
+                    ((uint32_t)d0[kQ8Bytes + 1] << 24);
+            }
+        }
+        out[i] = v;
     }
 }
 
 extern "C" int64_t idolq_q8_0_tiled_bytes(int64_t n, int64_t k) {
     if (n < 0 || k <= 0 || k % 64) return 0;
-    return (n + 127) / 128 * (k / 64) * 8704;
+    return (n + 31) / 32 * (k / 64) * 2176;
 }
 
 extern "C" int idolq_q8_0_tile(const uint8_t* w, int64_t n, int64_t k, uint8_t* out, void* stream) {
     if (n < 0 || k <= 0 || k % 64) return fail(IDOLQ_EINVAL, "tiled Q8_0 needs n >= 0 and k a positive multiple of 64");
     if (n == 0) return IDOLQ_OK;
     if (!w || !out) return fail(IDOLQ_EINVAL, "w and out must be non-null");
-    if ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(out)) & 3)
-        return fail(IDOLQ_EINVAL, "w and out must be 4-byte aligned");
+    if (reinterpret_cast<uintptr_t>(out) & 3) return fail(IDOLQ_EINVAL, "out must be 4-byte aligned");
     const int64_t total = idolq_q8_0_tiled_bytes(n, k) / 4;
-    hipLaunchKernelGGL(q8_tile_kernel, dim3(grid_for(total)), dim3(256), 0, static_cast<hipStream_t>(stream),
-                       reinterpret_cast<const uint32_t*>(w), n, (k / kQ8Block) * kQ8Bytes / 4, (int)(k / 64), total,
-                       reinterpret_cast<uint32_t*>(out));
-    return check_launch("q8_tile_kernel");
+    hipLaunchKernelGGL(q8_group_kernel, dim3(grid_for(total)), dim3(256), 0, static_cast<hipStream_t>(stream), w, n,
+                       (k / kQ8Block) * kQ8Bytes, (int)(k / 64), total, reinterpret_cast<uint32_t*>(out));
+    return check_launch("q8_group_kernel");
 }
 
 extern "C" int idolq_q8_0_quantize(const float* w, int64_t n, int64_t k, int64_t ldw, uint8_t* out, void* stream) {

@@ -26,7 +26,9 @@ struct GemmParams {
     int tiles_m, tiles_n;
     int x_aligned;  // x rows are 16-byte aligned
     int y_vec;      // y (and the residual, when given) rows and base are 16-byte aligned: vector epilogue stores
-    int w_tiled;    // w is in the tiled layout (idolq_q8_0_tile), p.w at the window's first tile
+    int w_tiled;    // w is in the grouped layout (idolq_q8_0_tile), p.w at the window's first 32-row group
+    int groups;     // grouped layout: 32-row groups from p.w to the end of the layout
+    int y_vec4;     // y, the residual and the bias allow vector access to 4-element groups
     // INT8 mode
     const int8_t* qa;
     const float* sa;
@@ -50,23 +52,16 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, i
     tn = in_group / gm;
 }
 
-// The pipelined DEQUANT kernel (q8_gemm_pipe.hip): 256 x 128 tiles, 16-bit activations with 16-byte aligned rows,
-// k a multiple of 64 and a 4-byte aligned weight window. One persistent workgroup per CU; with a workspace of
-// pipe_workspace_bytes() the tiles' k stages are split evenly over the workgroups (stream-K).
+// The pipelined DEQUANT kernel (q8_gemm_pipe.hip) on GGUF row-major weights: 256 x 128 tiles, 16-bit activations with
+// 16-byte aligned rows, k a multiple of 64 and a 4-byte aligned weight window; one persistent workgroup per CU.
 constexpr int kPipeBM = 256, kPipeBN = 128;
-
-struct PipeSplit {
-    int G;        // workgroups
-    int S;        // 64-deep stages per tile
-    int L, R;     // stream-K: workgroup r holds L + (r < R) stages
-    float* part;  // stream-K: G partial tiles (kPipeBM x kPipeBN fp32); null: whole tiles only
-    int* flags;   // G flags: workgroup r stores epoch when its partial tile is ready
-    int* error;   // set to 1 if a wait for a partial tile gave up
-    int epoch;    // launch number, never 0
-};
-
-size_t pipe_workspace_bytes();
 bool pipe_eligible(const GemmParams& p, int xt, int mode);
-int launch_pipe(GemmParams p, int xt, void* workspace, size_t workspace_bytes, hipStream_t stream);
+int launch_pipe(GemmParams p, int xt, hipStream_t stream);
+
+// The grouped-layout kernel (q8_gemm_wide.hip): 256 x 256 or 128 x 256 tiles, 4 waves; with a workspace of
+// wide_workspace_bytes() (zero-filled before first use) the leftover tiles' k stages may be split over the CUs.
+bool wide_eligible(const GemmParams& p, int xt, int mode);
+size_t wide_workspace_bytes();
+int launch_wide(GemmParams p, int xt, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 }  // namespace idolq

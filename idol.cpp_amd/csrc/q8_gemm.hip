@@ -17,6 +17,7 @@
 // lane l is row 8 * (r / 4) + 4 * (l / 32) + r % 4, column l % 32.
 #include "q8_gemm.h"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace idolq {
@@ -747,12 +748,12 @@ int launch_16bit(GemmParams p, int xt, int mode, bool w4, void* workspace, size_
     static const TileChoice cands[] = {{256, 128, 1.0f}, {128, 128, 0.5f}, {128, 64, 0.6f}};
     const TileChoice t = choose_tile(p.m, p.n, cands, 3);
     if (p.w_tiled) {
-        if (!pipe_eligible(p, xt, mode))
+        if (!wide_eligible(p, xt, mode))
             return fail(IDOLQ_EINVAL, "tiled weights need bf16/fp16 activations with 16-byte aligned rows and 16-byte "
                                       "aligned weights");
-        return launch_pipe(p, xt, workspace, workspace_bytes, stream);
+        return launch_wide(p, xt, workspace, workspace_bytes, stream);
     }
-    if (t.bm == 256 && pipe_eligible(p, xt, mode)) return launch_pipe(p, xt, workspace, workspace_bytes, stream);
+    if (t.bm == 256 && pipe_eligible(p, xt, mode)) return launch_pipe(p, xt, stream);
     if (t.bm == 256) return launch_16bit_tile<256, 128, 512>(p, xt, mode, w4, stream);
     if (t.bn == 128) return launch_16bit_tile<128, 128, kThreads>(p, xt, mode, w4, stream);
     return launch_16bit_tile<128, 64, kThreads>(p, xt, mode, w4, stream);
@@ -781,7 +782,7 @@ int quantize_act_launch(const void* x, int x_dtype, int64_t m, int64_t k, int64_
 using namespace idolq;
 
 extern "C" size_t idolq_q8_0_gemm_workspace(int64_t m, int64_t k, int mode) {
-    if (mode == IDOLQ_MODE_DEQUANT) return pipe_workspace_bytes();
+    if (mode == IDOLQ_MODE_DEQUANT) return wide_workspace_bytes();
     if (mode != IDOLQ_MODE_INT8 || m <= 0 || k <= 0 || k % kQ8Block) return 0;
     const size_t qa = ((size_t)m * (size_t)k + 255) / 256 * 256;
     return qa + (size_t)m * (size_t)(k / kQ8Block) * sizeof(float);
@@ -811,8 +812,8 @@ extern "C" int idolq_q8_0_gemm(const void* x, int x_dtype, int64_t m, int64_t k,
     if (mode == IDOLQ_MODE_DEQUANT && x_dtype == IDOLQ_F32)
         return fail(IDOLQ_EINVAL, "DEQUANT mode takes bf16 or fp16 activations");
     const bool tiled = (flags & IDOLQ_FLAG_TILED_WEIGHTS) != 0;
-    if (tiled && (mode != IDOLQ_MODE_DEQUANT || k % 64 || n_offset % 128))
-        return fail(IDOLQ_EINVAL, "tiled weights need DEQUANT mode, k a multiple of 64 and n_offset a multiple of 128");
+    if (tiled && (mode != IDOLQ_MODE_DEQUANT || k % 64 || n_offset % 32))
+        return fail(IDOLQ_EINVAL, "tiled weights need DEQUANT mode, k a multiple of 64 and n_offset a multiple of 32");
     if (m == 0 || n == 0) return IDOLQ_OK;  // empty input: nothing to read or write (pointers may be null)
     if (!x || !w || !y) return fail(IDOLQ_EINVAL, "x, w and y must be non-null");
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -821,8 +822,9 @@ extern "C" int idolq_q8_0_gemm(const void* x, int x_dtype, int64_t m, int64_t k,
     p.x = x;
     p.ldx = ldx;
     p.row_bytes = (k / kQ8Block) * kQ8Bytes;
-    p.w = tiled ? w + (n_offset / 128) * (k / 64) * 8704 : w + n_offset * p.row_bytes;
+    p.w = tiled ? w + (n_offset / 32) * (k / 64) * 2176 : w + n_offset * p.row_bytes;
     p.w_tiled = tiled ? 1 : 0;
+    p.groups = tiled ? (int)((n_total + 31) / 32 - n_offset / 32) : 0;
     p.m = (int)m;
     p.n = (int)n;
     p.k = (int)k;

@@ -20,9 +20,8 @@
 // Every buffer written in a stage was last read before the barrier that ended the previous stage. Rows of x beyond m
 // and weight rows beyond n read the last valid row instead (they only feed outputs that are never stored), so the
 // loads need no masks; k is a multiple of 64, so there is no partial stage.
-#include "q8_gemm.h"
+#include "q8_dma.h"
 
-#include <atomic>
 #include <string>
 #include <type_traits>
 
@@ -40,103 +39,6 @@ constexpr int kBBase = kRawBase + 3 * kRawBuf;        // 124416
 constexpr int kJunk = kBBase + 2 * kBBuf;             // 161280: 256 bytes that absorb the unused weight loads
 constexpr int kLdsBytes = kJunk + 256;                // 161536 (of 163840)
 static_assert(kLdsBytes <= 163840, "LDS budget");
-
-typedef __attribute__((address_space(3))) char lds_char;
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-
-template <typename T>
-struct PipeMfma;
-template <>
-struct PipeMfma<__bf16> {
-    typedef bf16x8 vec;
-    typedef bf16x2 pair;
-    static __device__ __forceinline__ f32x16 run(vec a, vec b, f32x16 c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-    }
-};
-template <>
-struct PipeMfma<_Float16> {
-    typedef f16x8 vec;
-    typedef f16x2 pair;
-    static __device__ __forceinline__ f32x16 run(vec a, vec b, f32x16 c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-    }
-};
-
-// Eight int8 codes (in a uint2) to eight operands T(fp32(d) * q), pairs rounded by one packed conversion.
-template <typename T>
-__device__ __forceinline__ uint4 dequant8(uint2 raw, float d) {
-    typedef typename PipeMfma<T>::pair T2;
-    uint32_t out[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const uint32_t word = e < 2 ? raw.x : raw.y;
-        const int sh = 16 * (e & 1);
-        f32x2 f;
-        f.x = (float)(int)(int8_t)(uint8_t)(word >> sh);
-        f.y = (float)(int)(int8_t)(uint8_t)(word >> (sh + 8));
-        out[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f * d, T2));
-    }
-    return make_uint4(out[0], out[1], out[2], out[3]);
-}
-
-// Four int8 codes (one dword) to four operands T(fp32(d) * q) (two packed pairs).
-template <typename T>
-__device__ __forceinline__ uint2 dequant4(uint32_t word, float d) {
-    typedef typename PipeMfma<T>::pair T2;
-    f32x2 lo, hi;
-    lo.x = (float)(int)(int8_t)(uint8_t)word;
-    lo.y = (float)(int)(int8_t)(uint8_t)(word >> 8);
-    hi.x = (float)(int)(int8_t)(uint8_t)(word >> 16);
-    hi.y = (float)(int)(int8_t)(uint8_t)(word >> 24);
-    return make_uint2(__builtin_bit_cast(uint32_t, __builtin_convertvector(lo * d, T2)),
-                      __builtin_bit_cast(uint32_t, __builtin_convertvector(hi * d, T2)));
-}
-
-// Direct global -> LDS loads (16 or 4 bytes per lane): lane i's bytes from base + off land at LDS address lds + 16 i
-// (4 i). Written as inline assembly so that the compiler, which cannot tell which LDS bytes such a load writes, does
-// not wait for every one of them before each LDS access; the kernel's explicit vmcnt waits and barriers order them.
-// base and lds are wave-uniform. The compiler does not see the vector-memory instruction inside the assembly, so
-// the assembly supplies the wait states itself: five, enough for an M0 or SGPR operand written just before by a
-// scalar or vector instruction (a vector write of an SGPR read by a vector-memory instruction needs five).
-// A wave-uniform pointer in scalar registers (the value must be the same in every lane).
-__device__ __forceinline__ const char* uniform_ptr(const char* ptr) {
-    const uint64_t v = reinterpret_cast<uint64_t>(ptr);
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-    return reinterpret_cast<const char*>(((uint64_t)hi << 32) | lo);
-}
-
-__device__ __forceinline__ void lds_dma16(const char* base, uint32_t off, uint32_t lds) {
-    asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
-}
-__device__ __forceinline__ void lds_dma4(const char* base, uint32_t off, uint32_t lds) {
-    asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
-}
-
-// s_waitcnt on the vector-memory counter only (expcnt and lgkmcnt left at their maximum).
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// One output element through the whole epilogue, any dtype and activation (the kernel's general path runs it in a
-// loop that is not unrolled, so its code exists once).
-__device__ __forceinline__ void epilogue_element(const GemmParams& p, int row, int col, float v) {
-    if ((p.flags & IDOLQ_FLAG_ROUND_BEFORE_BIAS) != 0) v = round_through(p.y_dt, v);
-    if (p.bias) v += load_as_float(p.bias, p.bias_dt, col);
-    if (p.res) v += load_as_float(p.res, p.res_dt, (int64_t)row * p.ldr + col);
-    store_from_float(p.y, p.y_dt, (int64_t)row * p.ldy + col, apply_act(p.act, v));
-}
-
-template <int ACT>
-__device__ __forceinline__ float act_fast(float v) {
-    if (ACT == IDOLQ_ACT_GELU_TANH) return apply_act(IDOLQ_ACT_GELU_TANH, v);
-    if (ACT == IDOLQ_ACT_RELU) return v > 0.0f ? v : 0.0f;
-    return v;
-}
 
 // The common epilogue: y and the residual (if any) of the activation dtype T, fp32 bias (if any), n a multiple of 4
 // and 4-element groups vector-aligned. All loads are issued (epilogue_loads) before the first store
@@ -198,8 +100,8 @@ __device__ __forceinline__ void epilogue_stores(const GemmParams& p, const f32x1
     }
 }
 
-template <typename T, bool TILED, bool SPLIT>
-__global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, int vec4, PipeSplit sp) {
+template <typename T>
+__global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, int vec4, int S) {
     typedef typename PipeMfma<T>::vec Vec;
     __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
 
@@ -228,8 +130,7 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
             w_off[j] = (uint32_t)((int64_t)row * p.row_bytes + (u % 17) * 4);
         }
         xg = uniform_ptr(static_cast<const char*>(p.x) + (size_t)k0 * 128);
-        wg = uniform_ptr(TILED ? reinterpret_cast<const char*>(p.w) + ((size_t)(n0 / kPipeBN) * (p.k / 64) + k0) * kRawBuf
-                               : reinterpret_cast<const char*>(p.w) + (size_t)k0 * 68);
+        wg = uniform_ptr(reinterpret_cast<const char*>(p.w) + (size_t)k0 * 68);
         nsteps = n;
     };
 
@@ -243,18 +144,7 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
     // 2176 dwords are 4.25 loads per wave: the fifth load of waves 2..7 reads a valid address into a junk area, so
     // every wave issues the same five loads (no branch, and the same vmcnt on every wave)
     const uint32_t w_dst4 = wave < (kRawUnits - 2048) / 64 ? kRawBase + 4 * 2048 + wave * 256 : kJunk;
-    // tiled weights: the stage's 8704 bytes are contiguous: 16 bytes per lane, 1 KB per wave, and the last 512 bytes
-    // by the first half of wave 0
-    auto issue_w_tiled_rest = [&](const char* base, int slot) __attribute__((always_inline)) {
-        if (wave == 0 && lane < 32) lds_dma16(base, (uint32_t)(8192 + lane * 16), lds0 + kRawBase + slot * kRawBuf + 8192);
-    };
     auto issue_w = [&](int s) __attribute__((always_inline)) {
-        if (TILED) {
-            const char* base = wg + (size_t)s * kRawBuf;
-            lds_dma16(base, (uint32_t)(tid * 16), lds0 + kRawBase + (s % 3) * kRawBuf + wave * 1024);
-            issue_w_tiled_rest(base, s % 3);
-            return;
-        }
         const char* base = wg + (size_t)s * 68;
         const uint32_t dst = lds0 + kRawBase + (s % 3) * kRawBuf + wave * 256;
 #pragma unroll
@@ -373,14 +263,13 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
         char* bdst = smem + kBBase + (s & 1) * kBBuf + cv_row * kBPitch + cv_q * 16;
         const char* abase = xg + (size_t)(s + 3) * 128;
         const uint32_t adst = lds0 + ((s + 3) % 3) * kABuf + wave * 1024;
-        const char* wbase = wg + (size_t)(s + 4) * (TILED ? kRawBuf : 68);
+        const char* wbase = wg + (size_t)(s + 4) * 68;
         const int wslot = (s + 4) % 3;
-        const uint32_t wdst = lds0 + kRawBase + wslot * kRawBuf + wave * (TILED ? 1024 : 256);
+        const uint32_t wdst = lds0 + kRawBase + wslot * kRawBuf + wave * 256;
         uint2 q0, q1, q2, q3;
 #define IDOLQ_SEGMENT(G, WORK)                                     \
         lds_dma16(abase, a_off[G], adst + G * 8192);               \
-        if (!TILED) lds_dma4(wbase, w_off[G], wdst + G * 2048);    \
-        if (TILED && G == 0) lds_dma16(wbase, (uint32_t)(tid * 16), wdst); \
+        lds_dma4(wbase, w_off[G], wdst + G * 2048);                \
         mfma_group(G);                                             \
         read_group(s + 1, G);                                      \
         WORK;                                                      \
@@ -405,15 +294,10 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
         IDOLQ_SEGMENT(3, q3 = dequant4<T>(raw.b1, d1);
                          *reinterpret_cast<uint4*>(bdst + 64) = make_uint4(q2.x, q2.y, q3.x, q3.y));
 #undef IDOLQ_SEGMENT
-        if (!TILED) lds_dma4(wbase, w_off[4], lds0 + w_dst4 + (w_dst4 == kJunk ? 0 : wslot * kRawBuf));
-        if (TILED) issue_w_tiled_rest(wbase, wslot);
+        lds_dma4(wbase, w_off[4], lds0 + w_dst4 + (w_dst4 == kJunk ? 0 : wslot * kRawBuf));
         // activations s + 2 and weight bytes s + 3 (issued in stage s - 1) have landed once at most the loads issued
-        // in this stage remain outstanding: 4 + 5 (raw weights), 4 + 1 (tiled; wave 0 issues one more and waits for
-        // one of this stage's loads too)
-        if (TILED)
-            wait_vm<5>();
-        else
-            wait_vm<9>();
+        // in this stage remain outstanding: 4 + 5
+        wait_vm<9>();
         __syncthreads();
     };
     auto stage_tail = [&](int s) __attribute__((always_inline)) {
@@ -468,126 +352,53 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
     }
     };
 
-    // ---- work: whole tiles (tiles r, r + G, ...) or, when sp.part is set, a contiguous range of the tiles' stages
-    // (stream-K): range r holds sp.L (+1 for r < sp.R) of the tiles * S stages in tile-major order, so every
-    // workgroup does the same work. A tile split across ranges is finished by the range holding its first stage:
-    // the ranges holding its other stages (each holds at most one such part: the first part of its range) store
-    // their fp32 partial tiles and raise their flags; the finishing range adds those partials before the epilogue.
+    // ---- work: whole tiles r, r + G, ... (groups of 8 row tiles walked column by column; the workgroups of one XCD
+    // take consecutive tiles, so those running together share weight and activation rows in that XCD's L2)
+    const int G = gridDim.x;
     int r = blockIdx.x;
-    if (sp.G % 8 == 0) r = (r % 8) * (sp.G / 8) + r / 8;  // ranges on one XCD are consecutive
+    if (G % 8 == 0) r = (r % 8) * (G / 8) + r / 8;
     const int ntiles = p.tiles_m * p.tiles_n;
     auto tile_at = [&](int t, int& m0, int& n0) __attribute__((always_inline)) {
-        constexpr int G8 = 8;  // groups of 8 row-tiles, walked column by column
+        constexpr int G8 = 8;
         const int per_group = G8 * p.tiles_n, group = t / per_group, first = group * G8;
         const int gm = min(p.tiles_m - first, G8), in_group = t - group * per_group;
         // integer division runs on the vector unit: bring the (uniform) results back to scalar registers
         m0 = __builtin_amdgcn_readfirstlane((first + in_group % gm) * kPipeBM);
         n0 = __builtin_amdgcn_readfirstlane((in_group / gm) * kPipeBN);
     };
-    if constexpr (!SPLIT) {
-        // With the register epilogue, the next tile's first loads are issued between the epilogue's loads and its
-        // arithmetic and stores, which hide their latency (the epilogue does not use LDS).
-        int m0 = 0, n0 = 0;
-        if (r < ntiles) {
-            tile_at(r, m0, n0);
-            start_segment(m0, n0, 0, sp.S);
-            prologue_issue();
-        }
-        for (int t = r; t < ntiles; t += sp.G) {
-            run_segment();
-            const int tn = t + sp.G, cm0 = m0, cn0 = n0;
-            if (fast_epilogue) {
-                const int row0 = cm0 + wm * 64 + (lane & 31), col0 = cn0 + wn * 64 + 4 * (lane >> 5);
-                EpilogueLoads L;
-                epilogue_loads(p, row0, col0, L);
-                // the epilogue's loads complete first: a compiler wait for one of them would otherwise also wait for
-                // the later loads issued below, which it cannot see
-                wait_vm<0>();
-                if (tn < ntiles) {
-                    tile_at(tn, m0, n0);
-                    start_segment(m0, n0, 0, sp.S);
-                    prologue_issue();
-                }
-                fast_stores(row0, col0, L);
-            } else {
-                epilogue(cm0, cn0);
-                __syncthreads();
-                if (tn < ntiles) {
-                    tile_at(tn, m0, n0);
-                    start_segment(m0, n0, 0, sp.S);
-                    prologue_issue();
-                }
-            }
-        }
-        return;
-    } else {
-    const int64_t begin = (int64_t)r * sp.L + min(r, sp.R);
-    const int64_t end = begin + sp.L + (r < sp.R ? 1 : 0);
-    // range holding global stage index i
-    auto owner = [&](int64_t i) __attribute__((always_inline)) {
-        const int64_t big = (int64_t)sp.R * (sp.L + 1);
-        return (int)(i < big ? i / (sp.L + 1) : sp.R + (i - big) / sp.L);
-    };
-    // Partial tiles and flags are written and read with device-scope (relaxed atomic) accesses, which go to the
-    // memory-side coherence point instead of the XCD's L2: no L2 write-back or invalidation (which would also evict
-    // the tiles other workgroups are streaming) is needed to pass them between XCDs.
-    typedef unsigned long long u64;
-    u64* const part = reinterpret_cast<u64*>(sp.part);
-    constexpr int kPartU64 = kPipeBM * kPipeBN / 2;
-    for (int64_t i = begin; i < end;) {
-        const int t = (int)(i / sp.S), k0 = (int)(i % sp.S);
-        const int n = (int)min((int64_t)(sp.S - k0), end - i);
-        int m0, n0;
-        tile_at(t, m0, n0);
-        start_segment(m0, n0, k0, n);
+    // With the register epilogue, the next tile's first loads are issued between the epilogue's loads and its
+    // arithmetic and stores, which hide their latency (the epilogue does not use LDS).
+    int m0 = 0, n0 = 0;
+    if (r < ntiles) {
+        tile_at(r, m0, n0);
+        start_segment(m0, n0, 0, S);
         prologue_issue();
-        run_segment();
-        if (k0 > 0) {
-            // a later part of the tile: store the partial accumulators (pair q of thread tid at q * 512 + tid), wait
-            // until they are written, then raise the flag
-#pragma unroll
-            for (int q = 0; q < 32; ++q) {
-                const f32x16& a = acc[q >> 4][(q >> 3) & 1];
-                const u64 v = ((u64)__float_as_uint(a[2 * (q & 7) + 1]) << 32) | __float_as_uint(a[2 * (q & 7)]);
-                __hip_atomic_store(part + (size_t)r * kPartU64 + q * kThreads + tid, v, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-            }
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
-            if (tid == 0) __hip_atomic_store(sp.flags + r, sp.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        } else {
-            if (n < sp.S) {
-                // the tile's first part: wait for the ranges holding the rest, add their partials
-                const int last = owner((int64_t)(t + 1) * sp.S - 1);
-                if (tid == 0) {
-                    for (int c = r + 1; c <= last; ++c) {
-                        int spins = 0;
-                        while (__hip_atomic_load(sp.flags + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != sp.epoch) {
-                            __builtin_amdgcn_s_sleep(4);
-                            if (++spins > (1 << 22)) {  // never expected: give up rather than hang
-                                __hip_atomic_store(sp.error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                                break;
-                            }
-                        }
-                    }
-                }
-                __syncthreads();
-                for (int c = r + 1; c <= last; ++c) {
-#pragma unroll
-                    for (int q = 0; q < 32; ++q) {
-                        const u64 v = __hip_atomic_load(part + (size_t)c * kPartU64 + q * kThreads + tid, __ATOMIC_RELAXED,
-                                                        __HIP_MEMORY_SCOPE_AGENT);
-                        f32x16& a = acc[q >> 4][(q >> 3) & 1];
-                        a[2 * (q & 7)] += __uint_as_float((unsigned)v);
-                        a[2 * (q & 7) + 1] += __uint_as_float((unsigned)(v >> 32));
-                    }
-                }
-            }
-            epilogue(m0, n0);
-        }
-        __syncthreads();
-        i += n;
     }
+    for (int t = r; t < ntiles; t += G) {
+        run_segment();
+        const int tn = t + G, cm0 = m0, cn0 = n0;
+        if (fast_epilogue) {
+            const int row0 = cm0 + wm * 64 + (lane & 31), col0 = cn0 + wn * 64 + 4 * (lane >> 5);
+            EpilogueLoads L;
+            epilogue_loads(p, row0, col0, L);
+            // the epilogue's loads complete first: a compiler wait for one of them would otherwise also wait for
+            // the later loads issued below, which it cannot see
+            wait_vm<0>();
+            if (tn < ntiles) {
+                tile_at(tn, m0, n0);
+                start_segment(m0, n0, 0, S);
+                prologue_issue();
+            }
+            fast_stores(row0, col0, L);
+        } else {
+            epilogue(cm0, cn0);
+            __syncthreads();
+            if (tn < ntiles) {
+                tile_at(tn, m0, n0);
+                start_segment(m0, n0, 0, S);
+                prologue_issue();
+            }
+        }
     }
 }
 
@@ -595,11 +406,10 @@ __global__ __launch_bounds__(kThreads) void q8_gemm_pipe_kernel(GemmParams p, in
 
 bool pipe_eligible(const GemmParams& p, int xt, int mode) {
     return mode == MODE_DEQUANT && (xt == XT_BF16 || xt == XT_F16) && p.x_aligned && p.k % 64 == 0 &&
-           p.row_bytes % 4 == 0 && (reinterpret_cast<uintptr_t>(p.w) & (p.w_tiled ? 15 : 3)) == 0 &&
+           !p.w_tiled && p.row_bytes % 4 == 0 && (reinterpret_cast<uintptr_t>(p.w) & 3) == 0 &&
            (int64_t)p.m * p.ldx * 2 < (int64_t)UINT32_MAX && (int64_t)p.n * p.row_bytes < (int64_t)UINT32_MAX;
 }
 
-namespace {
 int cu_count() {
     static int cached[64] = {0};
     int dev = 0;
@@ -611,68 +421,20 @@ int cu_count() {
     }
     return cached[dev];
 }
-std::atomic<int> g_epoch{0};
-}  // namespace
 
-// Partial tiles, flags and the error word for one workgroup per CU.
-size_t pipe_workspace_bytes() {
-    const size_t g = (size_t)cu_count();
-    return g * kPipeBM * kPipeBN * sizeof(float) + g * sizeof(int) + 256;
-}
-
-int launch_pipe(GemmParams p, int xt, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+int launch_pipe(GemmParams p, int xt, hipStream_t stream) {
     p.tiles_m = (p.m + kPipeBM - 1) / kPipeBM;
     p.tiles_n = (p.n + kPipeBN - 1) / kPipeBN;
     // 4-element groups of y, the residual and the bias are vector-accessible
     int vec4 = reinterpret_cast<uintptr_t>(p.y) % (4 * dtype_size(p.y_dt)) == 0 && p.ldy % 4 == 0;
     if (p.res) vec4 = vec4 && reinterpret_cast<uintptr_t>(p.res) % (4 * dtype_size(p.res_dt)) == 0 && p.ldr % 4 == 0;
     if (p.bias) vec4 = vec4 && reinterpret_cast<uintptr_t>(p.bias) % (4 * dtype_size(p.bias_dt)) == 0;
-
-    const int cus = cu_count();
-    const int tiles = p.tiles_m * p.tiles_n, S = p.k / 64;
-    const int64_t total = (int64_t)tiles * S;
-    PipeSplit sp{};
-    sp.S = S;
-    // stream-K when the tiles do not fill whole rounds of the CUs and a workspace is given
-    const bool split = workspace && workspace_bytes >= pipe_workspace_bytes() &&
-                       reinterpret_cast<uintptr_t>(workspace) % 256 == 0 && tiles % cus != 0 && total >= cus &&
-                       total / cus < INT32_MAX;
-    if (split) {
-        sp.G = cus;
-        sp.L = (int)(total / cus);
-        sp.R = (int)(total % cus);
-        sp.part = static_cast<float*>(workspace);
-        sp.flags = reinterpret_cast<int*>(static_cast<char*>(workspace) + (size_t)cus * kPipeBM * kPipeBN * sizeof(float));
-        sp.error = sp.flags + cus;
-        int e = g_epoch.fetch_add(1) + 1;
-        if (e <= 0) {  // wrapped: restart at 1
-            g_epoch.store(1);
-            e = 1;
-        }
-        sp.epoch = e;
-    } else {
-        sp.G = tiles < cus ? tiles : cus;
-    }
-    const dim3 grid(sp.G), block(kThreads);
-    void* fn = xt == XT_BF16 ? (p.w_tiled ? reinterpret_cast<void*>(&q8_gemm_pipe_kernel<__bf16, true, true>)
-                                          : reinterpret_cast<void*>(&q8_gemm_pipe_kernel<__bf16, false, true>))
-                             : (p.w_tiled ? reinterpret_cast<void*>(&q8_gemm_pipe_kernel<_Float16, true, true>)
-                                          : reinterpret_cast<void*>(&q8_gemm_pipe_kernel<_Float16, false, true>));
-    if (split) {
-        // a workgroup may wait for a later one: all must be resident at once
-        void* args[] = {&p, &vec4, &sp};
-        const hipError_t e = hipLaunchCooperativeKernel(fn, grid, block, args, 0, stream);
-        if (e != hipSuccess) return fail(IDOLQ_ELAUNCH, std::string("q8_gemm_pipe_kernel: ") + hipGetErrorString(e));
-        return check_launch("q8_gemm_pipe_kernel");
-    }
-#define IDOLQ_LAUNCH_PIPE(TT, TILED) \
-    hipLaunchKernelGGL((q8_gemm_pipe_kernel<TT, TILED, false>), grid, block, 0, stream, p, vec4, sp)
-    if (xt == XT_BF16) {
-        if (p.w_tiled) IDOLQ_LAUNCH_PIPE(__bf16, true); else IDOLQ_LAUNCH_PIPE(__bf16, false);
-    } else {
-        if (p.w_tiled) IDOLQ_LAUNCH_PIPE(_Float16, true); else IDOLQ_LAUNCH_PIPE(_Float16, false);
-    }
-#undef IDOLQ_LAUNCH_PIPE
+    const int cus = cu_count(), tiles = p.tiles_m * p.tiles_n, S = p.k / 64;
+    const dim3 grid(tiles < cus ? tiles : cus), block(kThreads);
+    if (xt == XT_BF16)
+        hipLaunchKernelGGL((q8_gemm_pipe_kernel<__bf16>), grid, block, 0, stream, p, vec4, S);
+    else
+        hipLaunchKernelGGL((q8_gemm_pipe_kernel<_Float16>), grid, block, 0, stream, p, vec4, S);
     return check_launch("q8_gemm_pipe_kernel");
 }
 

@@ -1,0 +1,618 @@
+// Q8_0 GEMM for gfx950 on the grouped weight layout (idolq_q8_0_tile), DEQUANT arithmetic: y = epilogue(x * W^T),
+// the MFMA operands being x (bf16 or fp16) and T(fp32(d) * q) for the Q8_0 weights, accumulated in fp32.
+//
+// Grouped layout. Weight rows in groups of 32 (the last group padded with zero rows), k in stages of 64 (two Q8_0
+// blocks); chunk (g, s) of 2176 bytes (32 rows x 68) at byte (g * S + s) * 2176, S = k / 64:
+//   [1024 b, 1024 b + 1024), b = 0, 1: the 32 codes of block b of each row in MFMA lane order: lane l's 16 bytes at
+//       16 l are, for row l % 32 and h = l / 32, codes 8 h .. 8 h + 7 of the block, then codes 16 + 8 h .. 16 + 8 h + 7
+//   [2048, 2176): 4 bytes per row r at 2048 + 4 r: the fp16 scale of block 0 (low half) and of block 1 (high half).
+// So one 16-byte load per lane fetches a block's MFMA operands for two 16-deep MFMA steps, and every load of a wave
+// reads 1 KB of contiguous bytes.
+//
+// Workgroup: 4 waves, one per SIMD, each owning all BM = 32 RT rows of the x tile and 32 CT weight rows (output
+// columns): RT x CT tiles of v_mfma_f32_32x32x16 accumulators (the transposed product C^T = W X^T, weights as the MFMA
+// rows, so accumulator element e of lane l is output row l % 32 and output column 8 (e / 4) + 4 (l / 32) + e % 4: four
+// consecutive columns per lane, stored as one vector). Tile BM x BN, BN = 128 CT. With RT = 8, CT = 2 a wave reads
+// 256 + 64 operand rows from LDS per 16 MFMAs: half the LDS bytes per MFMA of a 64 x 64 wave tile, which is what keeps
+// the LDS port (128 bytes per clock per CU) below the MFMA rate.
+//
+// Stage s covers k [64 s, 64 s + 64). Global memory reaches LDS without passing through registers
+// (global_load_lds_dwordx4):
+//   activations: BM rows x 128 bytes into one of three buffers, the eight 16-byte chunks of row r stored at chunk
+//       position c ^ ((r >> 1) & 7) (conflict-free MFMA operand reads); each wave loads a quarter of the rows;
+//   weights: each wave loads only its own CT groups (CT x 2 KB of codes + CT x 128 bytes of scales) into its own
+//       region of one of three buffers; no other wave reads them, so they need no barrier.
+// Each wave converts its weight codes in registers (T(fp32(d) * q), one MFMA step ahead) and reads its x operands
+// from LDS one MFMA step ahead. Stage s:
+//   issue weight loads of stage s + 2;
+//   steps 0..2: 16 MFMAs each, interleaved with the next step's x reads and weight conversion;
+//   wait until this wave's weight loads of stage s + 1 (and everything issued before them, which includes its
+//   activation loads of stage s + 1) have landed; barrier (every wave's share of activations s + 1 is in LDS and every
+//   wave has finished reading activation buffer s % 3); issue activation loads of stage s + 3 into buffer s % 3;
+//   step 3: 16 MFMAs, interleaved with the reads of stage s + 1's first x operands and weight bytes, then the
+//   conversion of its first weight operands.
+// Loads complete in issue order (A = activation loads of a stage, W = weight loads):
+//   prologue A0 W0 A1 W1 A2, then stage s issues W(s + 2) and A(s + 3),
+// so at the wait of stage s the loads issued after W(s + 1) are A(s + 2) and W(s + 2). Rows of x beyond m and weight
+// groups beyond the layout read the last valid row / group (they only feed outputs that are never stored).
+#include "q8_dma.h"
+
+#include <algorithm>
+#include <cstdlib>
+#include <string>
+#include <type_traits>
+#include <utility>
+
+namespace idolq {
+namespace {
+
+constexpr int kGroupBytes = 2176;  // one group (32 rows) x one stage (64 k)
+constexpr int kWideThreads = 256;  // 4 waves
+
+// Stream-K. The first dp tiles (a multiple of the G workgroups) are taken whole, round-robin. The k stages of the
+// other tiles, in tile-major order, are split into G contiguous ranges of L (the first R ranges L + 1) stages, one per
+// workgroup. A tile whose stages fall into several ranges is finished by the part that arrives last: a part that
+// finds the others already counted keeps its sum in registers; otherwise it stores its fp32 partial tile in its slot
+// of `part` (device-coherent stores) and counts itself in count[first range of the tile]. The part that sees the
+// count complete adds the stored partial tiles to its own (in range order), runs the epilogue and clears the count
+// for the next launch. Nobody waits for anybody, so the workgroups need not be resident together.
+struct WideSplit {
+    int G;        // workgroups
+    int dp;       // tiles taken whole
+    int L, R;     // stream-K ranges over the remaining tiles' stages; null part: whole tiles only
+    float* part;  // 2 G partial tiles: slot 2 r + f holds range r's first (f = 0) or last (f = 1) part
+    int* count;   // G counters, zero between launches (the workspace's first bytes)
+};
+
+template <int RT, int CT>
+struct WideCfg {
+    static constexpr int BM = 32 * RT, BN = 128 * CT;
+    static constexpr int ABuf = BM * 128;            // one stage of activations: BM rows x 64 16-bit values
+    static constexpr int WWave = CT * (2048 + 128);  // one stage of one wave's weight groups: codes, then scales
+    static constexpr int WBuf = 4 * WWave;
+    static constexpr int WBase = 3 * ABuf;
+    static constexpr int Lds = WBase + 3 * WBuf;
+    static constexpr int DA = BM / 32;               // activation loads (1 KB each) per wave per stage
+    static constexpr int DW = 2 * CT + 1;            // weight loads per wave per stage
+    static_assert(Lds <= 163840, "LDS budget");
+};
+
+// f(std::integral_constant<int, I>) for I = 0 .. N - 1, expanded at compile time (register-array indices stay constant)
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+template <typename T, int RT, int CT, int ACT, bool FAST, bool SPLIT>
+__global__ __launch_bounds__(kWideThreads) void q8_wide_kernel(GemmParams p, WideSplit sp) {
+    typedef WideCfg<RT, CT> C;
+    typedef typename PipeMfma<T>::vec Vec;
+    typedef typename PipeMfma<T>::pair T2;
+    constexpr int DA = C::DA, DW = C::DW;
+    __shared__ __attribute__((aligned(1024))) char smem[C::Lds];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int S = p.k / 64;  // stages of the whole depth
+    const int64_t gstride = (int64_t)S * kGroupBytes;
+    const uint32_t lds0 = (uint32_t)(size_t)(lds_char*)smem;
+    const char* xg;  // activations and weights of the segment's first stage
+    const char* wg;
+
+    // ---- per-tile load offsets (bytes, 32-bit)
+    // activations: load j of this wave fills LDS 16-byte chunks u = 64 (DA wave + j) + lane of the stage buffer:
+    // row u / 8, position u % 8, holding chunk (u % 8) ^ ((row >> 1) & 7) of the row
+    uint32_t a_off[DA], w_off[CT], ws_off;
+    auto start_tile = [&](int m0, int n0, int k0) __attribute__((always_inline)) {
+        xg = uniform_ptr(static_cast<const char*>(p.x) + (size_t)k0 * 128);
+        wg = uniform_ptr(reinterpret_cast<const char*>(p.w) + (size_t)k0 * kGroupBytes);
+#pragma unroll
+        for (int j = 0; j < DA; ++j) {
+            const int u = (wave * DA + j) * 64 + lane, row = u >> 3, c = (u & 7) ^ ((row >> 1) & 7);
+            a_off[j] = (uint32_t)((int64_t)min(m0 + row, p.m - 1) * p.ldx * 2 + c * 16);
+        }
+        const int g0 = n0 / 32 + wave * CT;
+#pragma unroll
+        for (int c = 0; c < CT; ++c) w_off[c] = (uint32_t)(min(g0 + c, p.groups - 1) * gstride + 16 * lane);
+        // scales: lanes 8 c .. 8 c + 7 fetch the 128 bytes of group c
+        ws_off = (uint32_t)(min(g0 + min(lane >> 3, CT - 1), p.groups - 1) * gstride + 2048 + 16 * (lane & 7));
+    };
+    // load j < DA of this wave's share of activation stage s
+    auto issue_a_piece = [&](int s, int j) __attribute__((always_inline)) {
+        lds_dma16(xg + (size_t)s * 128, a_off[j], lds0 + (s % 3) * C::ABuf + (wave * DA + j) * 1024);
+    };
+    auto issue_a = [&](int s) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < DA; ++j) issue_a_piece(s, j);
+    };
+    // load i < DW of this wave's weight stage s: block i % 2 of group i / 2, then (i = 2 CT) the scales
+    auto issue_w_piece = [&](int s, int i) __attribute__((always_inline)) {
+        const char* base = wg + (size_t)s * kGroupBytes;
+        const uint32_t dst = lds0 + C::WBase + (s % 3) * C::WBuf + wave * C::WWave;
+        if (i < 2 * CT)
+            lds_dma16(base + (i & 1) * 1024, w_off[i >> 1], dst + (i >> 1) * 2048 + (i & 1) * 1024);
+        else if (lane < 8 * CT)
+            lds_dma16(base, ws_off, dst + CT * 2048);
+    };
+    auto issue_w = [&](int s) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < DW; ++i) issue_w_piece(s, i);
+    };
+
+    // ---- MFMA operands
+    // x (MFMA columns): output row 32 rt + lane % 32, k = 16 j + 8 (lane / 32) .. + 7: chunk 2 j + lane / 32 of the row
+    uint32_t x_lane[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x_lane[j] = (lane & 31) * 128 + (((2 * j + (lane >> 5)) ^ ((lane >> 1) & 7)) * 16);
+    Vec xo[2][RT];     // x operands of two steps
+    uint4 wq[2][CT];   // weight operands of two steps (bits of Vec)
+    uint4 rc[CT][2];   // this stage's codes: group c, block b (two MFMA steps each)
+    uint32_t rs[CT];   // this stage's scales: group c, block 0 low / block 1 high
+    f32x16 acc[RT][CT];
+
+    auto read_x1 = [&](int buf, int j, int set, int rt) __attribute__((always_inline)) {
+        xo[set][rt] = *reinterpret_cast<const Vec*>(smem + buf * C::ABuf + x_lane[j] + rt * 4096);
+    };
+    // piece c < CT: the codes of group c; piece CT: the scales of every group
+    auto read_raw_piece = [&](int buf, int c) __attribute__((always_inline)) {
+        const char* wb = smem + C::WBase + buf * C::WBuf + wave * C::WWave;
+        if (c < CT) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b) rc[c][b] = *reinterpret_cast<const uint4*>(wb + c * 2048 + b * 1024 + 16 * lane);
+        } else {
+#pragma unroll
+            for (int g = 0; g < CT; ++g) rs[g] = *reinterpret_cast<const uint32_t*>(wb + CT * 2048 + g * 128 + 4 * (lane & 31));
+        }
+    };
+    // slice k < 2 CT of step j's weight operands: four codes (half k % 2 of group k / 2) to T(fp32(d) * q)
+    auto convert_slice = [&](int j, int set, int k) __attribute__((always_inline)) {
+        const int c = k >> 1, h = k & 1, b = j >> 1;
+        const float d = half_bits_to_float((uint16_t)(rs[c] >> (16 * b)));
+        const uint4 q = rc[c][b];
+        const uint2 o = dequant4<T>((j & 1) ? (h ? q.w : q.z) : (h ? q.y : q.x), d);
+        if (h) {
+            wq[set][c].z = o.x;
+            wq[set][c].w = o.y;
+        } else {
+            wq[set][c].x = o.x;
+            wq[set][c].y = o.y;
+        }
+    };
+    constexpr int NM = RT * CT;         // MFMAs per 16-deep step
+    constexpr int CV = NM - 2 * CT;     // first slot of the conversion slices
+    // One 16-deep step: MFMA i on operand set `cur`, then slot(i) -- the other work of the stage (loads, the next
+    // step's LDS reads and conversion) -- each slot pinned after its MFMA by a scheduling barrier, so that this work
+    // is issued while the matrix core runs the step instead of being moved next to its first use.
+    auto run_step = [&](int cur, auto slot) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < NM; ++i) {
+            acc[i / CT][i % CT] = PipeMfma<T>::run(__builtin_bit_cast(Vec, wq[cur][i % CT]), xo[cur][i / CT], acc[i / CT][i % CT]);
+            slot(i);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    // steps 0..2 of the stage in buffer buf (operands of step 0 in set 0); with ISSUE_W the weight loads of stage ws
+    // go out in the first slots
+    auto steps012 = [&](int buf, auto issue_w_tag, int ws) __attribute__((always_inline)) {
+        run_step(0, [&](int i) __attribute__((always_inline)) {
+            if constexpr (decltype(issue_w_tag)::value) {
+                if (i < DW) issue_w_piece(ws, i);
+            }
+            if (i < RT) read_x1(buf, 1, 1, i);
+            if (i >= CV) convert_slice(1, 1, i - CV);
+        });
+        run_step(1, [&](int i) __attribute__((always_inline)) {
+            if (i < RT) read_x1(buf, 2, 0, i);
+            if (i >= CV) convert_slice(2, 0, i - CV);
+        });
+        run_step(0, [&](int i) __attribute__((always_inline)) {
+            if (i < RT) read_x1(buf, 3, 1, i);
+            if (i >= CV) convert_slice(3, 1, i - CV);
+        });
+    };
+    // step 3 and the first operands of the next stage (buffers nb): its weight bytes, x operands and the conversion
+    // of its first weight operands; with ISSUE_A the activation loads of stage as go out in the first slots
+    auto step3_next = [&](int nb, auto issue_a_tag, int as) __attribute__((always_inline)) {
+        run_step(1, [&](int i) __attribute__((always_inline)) {
+            if constexpr (decltype(issue_a_tag)::value) {
+                if (i < DA) issue_a_piece(as, i);
+            }
+            if (i <= CT)
+                read_raw_piece(nb, i);
+            else if (i <= CT + RT)
+                read_x1(nb, 0, 0, i - CT - 1);
+            if (i >= CV) convert_slice(0, 0, i - CV);
+        });
+    };
+
+    // ---- epilogue
+    // Each wave's fp32 accumulators go through LDS, CH row tiles at a time (rows of 32 CT columns, pitch EP floats, in
+    // the activation buffers, free once every wave has finished the last stage), and come back row-major: LPR lanes
+    // per row, 4 columns each, so that the residual loads and the output stores move whole rows of the wave's 32 CT
+    // columns (every cache line written whole) instead of 8-byte pieces of 32 rows.
+    // FAST (chosen by the host): y and the residual have the activation dtype, the bias is fp32, n is a multiple of 4
+    // with vector-aligned 4-column groups, and the activation is ACT; rows and 4-column groups outside y are skipped.
+    // Otherwise the general path: per element bounds checks and dtype conversions.
+    const bool round_first = (p.flags & IDOLQ_FLAG_ROUND_BEFORE_BIAS) != 0;
+    constexpr int CH = RT >= 8 ? 2 : 1;   // row tiles per chunk
+    constexpr int EP = 32 * CT + 4;       // floats per staged row (the 4-float pad spreads the 16-byte writes of 16
+                                          // consecutive rows over distinct banks)
+    constexpr int ER = 32 * CH;           // rows per chunk
+    constexpr int LPR = 8 * CT;           // read-back lanes per row
+    constexpr int RPI = 64 / LPR;         // rows per read-back instruction
+    constexpr int NR = ER / RPI;          // read-back instructions per chunk
+    constexpr int NQ = RT / CH;           // chunks
+    static_assert(4 * ER * EP * 4 <= C::Lds, "epilogue staging fits in LDS");
+    // chunk q of the accumulators to the wave's staging rows; the reads that follow take values other lanes wrote:
+    // the wave's LDS operations run in order, and the fences keep the compiler from moving the reads above the writes
+    auto stage_chunk = [&](float* st, auto qtag) __attribute__((always_inline)) {
+        constexpr int q = decltype(qtag)::value;
+#pragma unroll
+        for (int h = 0; h < CH; ++h)
+#pragma unroll
+            for (int c = 0; c < CT; ++c)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const f32x16& a = acc[CH * q + h][c];
+                    *reinterpret_cast<float4*>(st + (32 * h + (lane & 31)) * EP + 32 * c + 8 * g + 4 * (lane >> 5)) =
+                        make_float4(a[4 * g], a[4 * g + 1], a[4 * g + 2], a[4 * g + 3]);
+                }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    auto chunk_done = [&]() __attribute__((always_inline)) {  // the next chunk reuses the staging rows just read
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    auto fast_epilogue = [&](int m0, int n0) __attribute__((always_inline)) {
+        float* const st = reinterpret_cast<float*>(smem) + wave * ER * EP;
+        const int rl = lane / LPR, cl = lane % LPR;
+        const int col = n0 + wave * 32 * CT + 4 * cl;
+        // loads read clamped (valid) addresses, so only the stores carry bounds checks (n is a multiple of 4)
+        const bool col_ok = col < p.n;
+        const int lcol = min(col, p.n - 4);
+        const float4 b = p.bias ? *reinterpret_cast<const float4*>(static_cast<const float*>(p.bias) + lcol)
+                                : make_float4(0, 0, 0, 0);
+        // the residual loads of the first PD chunks go out first, those of chunk q + PD before chunk q's stores (a
+        // wait for a load then never includes a store); PD = every chunk where the registers allow
+        constexpr int PD = NQ * NR <= 32 ? NQ : 2;
+        uint2 r2[PD][NR];
+        auto load_res = [&](int q) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < NR; ++i) {
+                const int row = min(m0 + ER * q + RPI * i + rl, p.m - 1);
+                r2[q % PD][i] = p.res ? *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.res) + (int64_t)row * p.ldr + lcol)
+                                      : make_uint2(0, 0);
+            }
+        };
+#pragma unroll
+        for (int q = 0; q < PD; ++q) load_res(q);
+        __syncthreads();  // every wave has finished reading the activation buffers
+        static_for<NQ>([&](auto qtag) __attribute__((always_inline)) {
+            constexpr int q = decltype(qtag)::value;
+            if (q >= 1 && q - 1 + PD < NQ) load_res(q - 1 + PD);
+            stage_chunk(st, qtag);
+#pragma unroll
+            for (int i = 0; i < NR; ++i) {
+                const int lrow = RPI * i + rl, row = m0 + ER * q + lrow;
+                const float4 v4 = *reinterpret_cast<const float4*>(st + lrow * EP + 4 * cl);
+                f32x2 lo = {v4.x, v4.y}, hi = {v4.z, v4.w};
+                if (round_first) {
+                    lo = __builtin_convertvector(__builtin_convertvector(lo, T2), f32x2);
+                    hi = __builtin_convertvector(__builtin_convertvector(hi, T2), f32x2);
+                }
+                const uint2 rr = r2[q % PD][i];
+                lo = lo + f32x2{b.x, b.y} + __builtin_convertvector(__builtin_bit_cast(T2, rr.x), f32x2);
+                hi = hi + f32x2{b.z, b.w} + __builtin_convertvector(__builtin_bit_cast(T2, rr.y), f32x2);
+                lo = f32x2{act_fast<ACT>(lo.x), act_fast<ACT>(lo.y)};
+                hi = f32x2{act_fast<ACT>(hi.x), act_fast<ACT>(hi.y)};
+                if (col_ok && row < p.m)
+                    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.y) + (int64_t)row * p.ldy + col) =
+                        make_uint2(__builtin_bit_cast(uint32_t, __builtin_convertvector(lo, T2)),
+                                   __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, T2)));
+            }
+            chunk_done();
+        });
+    };
+    auto general_epilogue = [&](int m0, int n0) __attribute__((always_inline)) {
+        float* const st = reinterpret_cast<float*>(smem) + wave * ER * EP;
+        const int rl = lane / LPR, cl = lane % LPR;
+        const int col = n0 + wave * 32 * CT + 4 * cl;
+        __syncthreads();  // every wave has finished reading the activation buffers
+        static_for<NQ>([&](auto qtag) __attribute__((always_inline)) {
+            constexpr int q = decltype(qtag)::value;
+            stage_chunk(st, qtag);
+#pragma unroll 1
+            for (int i = 0; i < NR * 4; ++i) {
+                const int lrow = RPI * (i >> 2) + rl, row = m0 + ER * q + lrow, cc = col + (i & 3);
+                if (row < p.m && cc < p.n) {
+                    float x = st[lrow * EP + 4 * cl + (i & 3)];
+                    if (round_first) x = round_through(p.y_dt, x);
+                    if (p.bias) x += load_as_float(p.bias, p.bias_dt, cc);
+                    if (p.res) x += load_as_float(p.res, p.res_dt, (int64_t)row * p.ldr + cc);
+                    store_from_float(p.y, p.y_dt, (int64_t)row * p.ldy + cc, apply_act(p.act, x));
+                }
+            }
+            chunk_done();
+        });
+    };
+    auto epilogue = [&](int m0, int n0) __attribute__((always_inline)) {
+        if constexpr (FAST)
+            fast_epilogue(m0, n0);
+        else
+            general_epilogue(m0, n0);
+    };
+
+    // ---- one segment: stages k0 .. k0 + S - 1 of the tile at (m0, n0), accumulated from zero into acc
+    auto run_segment = [&](int m0, int n0, int k0, int S) __attribute__((always_inline)) {
+        start_tile(m0, n0, k0);
+        __syncthreads();  // every wave is done with the previous segment's LDS
+        issue_a(0);
+        issue_w(0);
+        if (S > 1) {
+            issue_a(1);
+            issue_w(1);
+        }
+        if (S > 2) issue_a(2);
+#pragma unroll
+        for (int i = 0; i < RT; ++i)
+#pragma unroll
+            for (int j = 0; j < CT; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+        // W0 (and A0 before it) landed: A1, W1, A2 may remain
+        if (S > 2)
+            wait_vm<2 * DA + DW>();
+        else if (S > 1)
+            wait_vm<DA + DW>();
+        else
+            wait_vm<0>();
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c <= CT; ++c) read_raw_piece(0, c);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) read_x1(0, 0, 0, rt);
+#pragma unroll
+        for (int k = 0; k < 2 * CT; ++k) convert_slice(0, 0, k);
+
+        const std::true_type issue;
+        const std::false_type no_issue;
+        int s = 0;
+        for (; s + 3 < S; ++s) {
+            steps012(s % 3, issue, s + 2);
+            wait_vm<DA + DW>();  // W(s + 1): A(s + 2), W(s + 2) may remain
+            __syncthreads();
+            step3_next((s + 1) % 3, issue, s + 3);
+        }
+        if (s + 3 == S) {  // W(s + 2) is the last weight stage; no more activation loads
+            steps012(s % 3, issue, s + 2);
+            wait_vm<DA + DW>();
+            __syncthreads();
+            step3_next((s + 1) % 3, no_issue, 0);
+            ++s;
+        }
+        if (s + 2 == S) {  // nothing issued after W(s + 1)
+            steps012(s % 3, no_issue, 0);
+            wait_vm<0>();
+            __syncthreads();
+            step3_next((s + 1) % 3, no_issue, 0);
+            ++s;
+        }
+        // last stage
+        steps012(s % 3, no_issue, 0);
+        run_step(1, [](int) {});
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // tile t: groups of 8 row tiles walked column by column
+    auto tile_at = [&](int t, int& m0, int& n0) __attribute__((always_inline)) {
+        constexpr int G8 = 8;
+        const int per_group = G8 * p.tiles_n, group = t / per_group, first = group * G8;
+        const int gm = min(p.tiles_m - first, G8), in_group = t - group * per_group;
+        m0 = __builtin_amdgcn_readfirstlane((first + in_group % gm) * C::BM);
+        n0 = __builtin_amdgcn_readfirstlane((in_group / gm) * C::BN);
+    };
+
+    // ---- the workgroups on one XCD (b % 8) take consecutive tiles / ranges, so those running together share
+    // activation and weight rows in that XCD's L2
+    const int G = gridDim.x;
+    int r = blockIdx.x;
+    if (G % 8 == 0) r = (r % 8) * (G / 8) + r / 8;
+    const int ntiles = p.tiles_m * p.tiles_n;
+    if constexpr (!SPLIT) {
+        for (int t = r; t < ntiles; t += G) {
+            int m0, n0;
+            tile_at(t, m0, n0);
+            run_segment(m0, n0, 0, S);
+            epilogue(m0, n0);
+        }
+    } else {
+        for (int t = r; t < sp.dp; t += G) {
+            int m0, n0;
+            tile_at(t, m0, n0);
+            run_segment(m0, n0, 0, S);
+            epilogue(m0, n0);
+        }
+        // partial tiles: uint4 q (floats 4 (q % 4) .. of accumulator tile q / 4) of thread tid at byte
+        // (q * 256 + tid) * 16 of the slot
+        constexpr int kQ = RT * CT * 4;
+        constexpr int kSlot = C::BM * C::BN * 4;
+        const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(sp.part, 0, 2 * G * kSlot, 0x00020000);
+        constexpr int kCoherent = 16;  // sc1: device scope, through to the coherence point shared by all XCDs
+        const int64_t big = (int64_t)sp.R * (sp.L + 1);
+        auto begin_of = [&](int c) __attribute__((always_inline)) { return (int64_t)c * sp.L + min(c, sp.R); };
+        auto owner = [&](int64_t i) __attribute__((always_inline)) {
+            return (int)(i < big ? i / (sp.L + 1) : sp.R + (i - big) / sp.L);
+        };
+        __shared__ int arrivals;
+        const int64_t begin = begin_of(r), end = begin + sp.L + (r < sp.R ? 1 : 0);
+        for (int64_t i = begin; i < end;) {
+            const int tl = (int)(i / S), k0 = (int)(i - (int64_t)tl * S);
+            const int n = (int)min((int64_t)(S - k0), end - i);
+            int m0, n0;
+            tile_at(sp.dp + tl, m0, n0);
+            run_segment(m0, n0, k0, n);
+            if (n < S) {
+                const int64_t t0 = (int64_t)tl * S;
+                const int first = owner(t0), last = owner(t0 + S - 1);
+                if (tid == 0) arrivals = __hip_atomic_load(sp.count + first, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __syncthreads();
+                bool finish = arrivals == last - first;
+                __syncthreads();
+                if (!finish) {
+                    const int off = (2 * r + (i > begin ? 1 : 0)) * kSlot + tid * 16;
+#pragma unroll
+                    for (int q = 0; q < kQ; ++q) {
+                        const f32x16& a = acc[(q >> 2) / CT][(q >> 2) % CT];
+                        const f32x4 v = {a[4 * (q & 3)], a[4 * (q & 3) + 1], a[4 * (q & 3) + 2], a[4 * (q & 3) + 3]};
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), prs, off + q * 4096, 0, kCoherent);
+                    }
+                    // the stores have reached the coherence point before the count moves
+                    __builtin_amdgcn_s_waitcnt(0);
+                    __syncthreads();
+                    if (tid == 0)
+                        arrivals = __hip_atomic_fetch_add(sp.count + first, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __syncthreads();
+                    finish = arrivals == last - first;
+                }
+                if (finish) {
+                    // every other part is stored: add them (range order), two accumulator tiles per batch of loads
+                    for (int c = first; c <= last; ++c) {
+                        if (c == r) continue;
+                        const int off = (2 * c + (t0 > begin_of(c) ? 1 : 0)) * kSlot + tid * 16;
+#pragma unroll
+                        for (int q0 = 0; q0 < kQ; q0 += 8) {
+                            i32x4 v[8];
+#pragma unroll
+                            for (int q = 0; q < 8; ++q)
+                                v[q] = __builtin_amdgcn_raw_buffer_load_b128(prs, off + (q0 + q) * 4096, 0, kCoherent);
+#pragma unroll
+                            for (int q = 0; q < 8; ++q) {
+                                f32x16& a = acc[((q0 + q) >> 2) / CT][((q0 + q) >> 2) % CT];
+                                const f32x4 f = __builtin_bit_cast(f32x4, v[q]);
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) a[4 * ((q0 + q) & 3) + e] += f[e];
+                            }
+                        }
+                    }
+                    if (tid == 0) __hip_atomic_store(sp.count + first, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    epilogue(m0, n0);
+                }
+            } else {
+                epilogue(m0, n0);
+            }
+            i += n;
+        }
+    }
+}
+
+template <typename T, int RT, int CT, bool SPLIT>
+int launch_wide_s(GemmParams p, const WideSplit& sp, hipStream_t stream) {
+    const dim3 grid(sp.G), block(kWideThreads);
+    p.tiles_m = (p.m + 32 * RT - 1) / (32 * RT);
+    p.tiles_n = (p.n + 128 * CT - 1) / (128 * CT);
+    constexpr int kYdt = std::is_same<T, __bf16>::value ? IDOLQ_BF16 : IDOLQ_F16;
+    const bool fast = p.y_vec4 && p.n % 4 == 0 && p.y_dt == kYdt && (!p.res || p.res_dt == kYdt) &&
+                      (!p.bias || p.bias_dt == IDOLQ_F32) &&
+                      (p.act == IDOLQ_ACT_NONE || p.act == IDOLQ_ACT_GELU_TANH || p.act == IDOLQ_ACT_RELU);
+    // the register epilogue's activation is a template argument; other activations take the general path
+    if (!fast)
+        hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, IDOLQ_ACT_NONE, false, SPLIT>), grid, block, 0, stream, p, sp);
+    else if (p.act == IDOLQ_ACT_GELU_TANH)
+        hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, IDOLQ_ACT_GELU_TANH, true, SPLIT>), grid, block, 0, stream, p, sp);
+    else if (p.act == IDOLQ_ACT_RELU)
+        hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, IDOLQ_ACT_RELU, true, SPLIT>), grid, block, 0, stream, p, sp);
+    else
+        hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, IDOLQ_ACT_NONE, true, SPLIT>), grid, block, 0, stream, p, sp);
+    return check_launch("q8_wide_kernel");
+}
+
+// Workspace: tile counters in the first kCountBytes, then the partial tiles.
+constexpr size_t kCountBytes = 4096;
+
+// The columns [n0, n0 + n) of a launch (multiples of 32).
+GemmParams column_window(GemmParams p, int n0, int n) {
+    const int S = p.k / 64;
+    p.w += (size_t)(n0 / 32) * S * kGroupBytes;
+    p.groups -= n0 / 32;
+    if (p.bias) p.bias = static_cast<const char*>(p.bias) + (size_t)n0 * dtype_size(p.bias_dt);
+    if (p.res) p.res = static_cast<const char*>(p.res) + (size_t)n0 * dtype_size(p.res_dt);
+    p.y = static_cast<char*>(p.y) + (size_t)n0 * dtype_size(p.y_dt);
+    p.n = n;
+    return p;
+}
+
+// Launch plans, costed in microseconds from MI355X measurements (4096 x 4096 outputs): a 64-deep stage of a round of
+// tiles takes 1.42 (256-row tiles) / 0.85 (128-row tiles); a tile's fixed part (first loads; the epilogue, where the
+// whole round's outputs are written at once, at the memory's write rate) 16 / 9.
+//   whole tiles, 256 or 128 rows;
+//   columns split in two launches: whole rounds of 256-row tiles on the first columns, 128-row tiles on the rest
+//     (fills the CUs when 256-row tiles would leave a partial round);
+//   128-row tiles with stream-K over the tiles left after the whole rounds (a workspace is needed; about 6 more for
+//     the partial tiles). 256-row tiles are not split: their splits lose the L2 sharing of neighbouring workgroups.
+template <typename T>
+int launch_wide_dtype(GemmParams p, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    const long cus = cu_count(), S = p.k / 64;
+    const long tm8 = (p.m + 255) / 256, tm4 = (p.m + 127) / 128, tn = (p.n + 255) / 256;
+    auto rounds = [&](long tiles) { return (tiles + cus - 1) / cus; };
+    const double c8 = S * 1.42 + 16.0, c4 = S * 0.85 + 9.0;
+    const double whole8 = rounds(tm8 * tn) * c8, whole4 = rounds(tm4 * tn) * c4;
+    // split columns: as many column blocks as fill whole rounds of 256-row tiles, the rest with 128-row tiles
+    const long cb8 = (tm8 * tn) / cus * cus / tm8;  // column blocks of the first launch (whole rounds when tm8 divides)
+    const double hybrid = cb8 > 0 && cb8 < tn ? rounds(tm8 * cb8) * c8 + rounds(tm4 * (tn - cb8)) * c4 + 4.0 : -1.0;
+    const long dp4 = tm4 * tn / cus * cus, units = (tm4 * tn - dp4) * S;
+    const bool can_split = workspace && workspace_bytes >= kCountBytes + (size_t)2 * cus * 128 * 256 * 4 && units >= cus;
+    const double split4 = can_split ? (double)dp4 / cus * c4 + (double)rounds(units) * 0.85 + 2 * 9.0 + 6.0 : -1.0;
+
+    double best = whole8;
+    int plan = 0;
+    if (whole4 < best) best = whole4, plan = 1;
+    if (hybrid > 0 && hybrid < best) best = hybrid, plan = 2;
+    if (split4 > 0 && split4 < best) best = split4, plan = 3;
+    const WideSplit none{0, 0, 0, 0, nullptr, nullptr};
+    auto whole = [&](long tiles) { WideSplit sp = none; sp.G = (int)std::min(tiles, cus); return sp; };
+    switch (plan) {
+        case 0: return launch_wide_s<T, 8, 2, false>(p, whole(tm8 * tn), stream);
+        case 1: return launch_wide_s<T, 4, 2, false>(p, whole(tm4 * tn), stream);
+        case 2: {
+            const int n1 = (int)cb8 * 256;
+            int rc = launch_wide_s<T, 8, 2, false>(column_window(p, 0, n1), whole(tm8 * cb8), stream);
+            if (rc) return rc;
+            return launch_wide_s<T, 4, 2, false>(column_window(p, n1, p.n - n1), whole(tm4 * (tn - cb8)), stream);
+        }
+        default: {
+            WideSplit sp{(int)cus, (int)dp4, (int)(units / cus), (int)(units % cus),
+                         reinterpret_cast<float*>(static_cast<char*>(workspace) + kCountBytes), static_cast<int*>(workspace)};
+            return launch_wide_s<T, 4, 2, true>(p, sp, stream);
+        }
+    }
+}
+
+}  // namespace
+
+bool wide_eligible(const GemmParams& p, int xt, int mode) {
+    return mode == MODE_DEQUANT && (xt == XT_BF16 || xt == XT_F16) && p.w_tiled && p.x_aligned && p.k % 64 == 0 &&
+           (reinterpret_cast<uintptr_t>(p.w) & 15) == 0 && p.groups > 0 &&
+           (int64_t)p.m * p.ldx * 2 < (int64_t)UINT32_MAX &&
+           (int64_t)p.groups * (p.k / 64) * kGroupBytes < (int64_t)UINT32_MAX;
+}
+
+size_t wide_workspace_bytes() { return kCountBytes + (size_t)2 * cu_count() * 128 * 256 * 4; }
+
+int launch_wide(GemmParams p, int xt, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    // 4-element groups of y, the residual and the bias are vector-accessible
+    int vec4 = reinterpret_cast<uintptr_t>(p.y) % (4 * dtype_size(p.y_dt)) == 0 && p.ldy % 4 == 0;
+    if (p.res) vec4 = vec4 && reinterpret_cast<uintptr_t>(p.res) % (4 * dtype_size(p.res_dt)) == 0 && p.ldr % 4 == 0;
+    if (p.bias) vec4 = vec4 && reinterpret_cast<uintptr_t>(p.bias) % (4 * dtype_size(p.bias_dt)) == 0;
+    p.y_vec4 = vec4;
+    if (workspace && reinterpret_cast<uintptr_t>(workspace) % 256 != 0) workspace = nullptr;
+    if (xt == XT_BF16) return launch_wide_dtype<__bf16>(p, workspace, workspace_bytes, stream);
+    return launch_wide_dtype<_Float16>(p, workspace, workspace_bytes, stream);
+}
+
+}  // namespace idolq

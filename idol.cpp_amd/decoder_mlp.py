@@ -11,8 +11,9 @@ The embedding follows src/decoders.cpp:215-230 (coordinate by coordinate, sines 
 with the frequencies 2^linspace(0, 10, 16) of tools/gguf_to_decoder.py:82-84.
 
 On the GPU the activations between layers are bf16 (the Q8_0 linears run in DEQUANT arithmetic) and the head is fp32.
-The first layer's depth is padded from 352 to 384 with zero blocks (and zero input columns) so that every Q8_0 layer
-reads the tiled weight layout; the padding adds exact zeros. All buffers are allocated once per point count.
+The first layer's depth is padded from 352 to 384 with zero blocks (and zero input columns) so that the 256-wide layers
+read the tiled weight layout (256-column tiles); the padding adds exact zeros. The 64-wide third layer reads the GGUF
+row-major blocks, whose kernel tiles 128 (or 64) columns. All buffers are allocated once per point count.
 """
 import torch
 
@@ -34,7 +35,8 @@ class PointMLP:
         self.k1 = feat + 6 * nfreq
         self.k1pad = (self.k1 + 63) // 64 * 64
         self.freqs = torch.pow(2.0, torch.linspace(0.0, 10.0, nfreq, dtype=torch.float32)).to(device)
-        # Q8_0 weights as GGUF row-major blocks (w) and in the tiled layout (wt); layer 1 zero-padded in depth
+        # Q8_0 weights as GGUF row-major blocks (w) and, for the 256-wide layers, in the tiled layout (wt); layer 1
+        # zero-padded in depth
         self.shape = {"l1": (hidden, self.k1), "l2": (hidden, hidden), "l3": (mid, hidden)}
         self.w, self.b = {}, {}
         for name, (n, k) in self.shape.items():
@@ -46,8 +48,7 @@ class PointMLP:
         w1 = self.w["l1"].view(hidden, self.k1 // 32, 34)
         w1pad = torch.cat([w1, torch.zeros((hidden, pad_blocks, 34), dtype=torch.uint8, device=device)], dim=1)
         self.wt = {"l1": L.tile_q8_0(w1pad.reshape(-1).contiguous(), hidden, self.k1pad),
-                   "l2": L.tile_q8_0(self.w["l2"], hidden, hidden),
-                   "l3": L.tile_q8_0(self.w["l3"], mid, hidden)}
+                   "l2": L.tile_q8_0(self.w["l2"], hidden, hidden)}
         self._m = None
 
     def _buffers(self, m):
@@ -74,7 +75,7 @@ class PointMLP:
         relu, dq = L.ACT_RELU, L.MODE_DEQUANT
         L.gemm(x, self.wt["l1"], self.hidden, bias=self.b["l1"], act=relu, mode=dq, out=self.h1, tiled=True)
         L.gemm(self.h1, self.wt["l2"], self.hidden, bias=self.b["l2"], act=relu, mode=dq, out=self.h2, tiled=True)
-        L.gemm(self.h2, self.wt["l3"], self.mid, bias=self.b["l3"], act=relu, mode=dq, out=self.h3, tiled=True)
+        L.gemm(self.h2, self.w["l3"], self.mid, bias=self.b["l3"], act=relu, mode=dq, out=self.h3)
         return L.linear_f32(self.h3, self.head_w, self.head_b, out=self.y)
 
     def flop(self, m):

@@ -47,7 +47,7 @@ class DenoiserLayer:
         n, _ = self.shape[name]
         if mode == L.MODE_DEQUANT and name in self.wt:
             return L.gemm(x, self.wt[name], n, bias=self.b[name], act=act, residual=residual, mode=mode, out=out,
-                          tiled=True)
+                          tiled=True, split=True)
         return L.gemm(x, self.w[name], n, bias=self.b[name], act=act, residual=residual, mode=mode, out=out)
 
 

@@ -37,7 +37,7 @@ enum { IDOLQ_MODE_AUTO = 0, IDOLQ_MODE_DEQUANT = 1, IDOLQ_MODE_EXACT = 2, IDOLQ_
 
 /* GEMM flags. ROUND_BEFORE_BIAS rounds the product to the output dtype before the bias is added, as the reference's
  * fused GPU path does (tools/idol_triton.py:84-89). TILED_WEIGHTS: w is in the tiled Q8_0 layout written by
- * idolq_q8_0_tile (DEQUANT mode, bf16/fp16 activations with 16-byte aligned rows, k % 64 == 0, n_offset % 128 == 0). */
+ * idolq_q8_0_tile (DEQUANT mode, bf16/fp16 activations with 16-byte aligned rows, k % 64 == 0, n_offset % 32 == 0). */
 enum { IDOLQ_FLAG_ROUND_BEFORE_BIAS = 1, IDOLQ_FLAG_TILED_WEIGHTS = 2 };
 
 enum {
@@ -65,9 +65,10 @@ int64_t idolq_q8_0_bytes(int64_t n, int64_t k);
  *   act      IDOLQ_ACT_*, applied after bias and residual
  *   y        [m x n] in y_dtype, row stride ldy
  *   workspace / workspace_bytes  scratch of idolq_q8_0_gemm_workspace bytes: required by IDOLQ_MODE_INT8 (quantized
- *            activations); optional for IDOLQ_MODE_DEQUANT, where it lets the k stages of the tiles be split evenly
- *            over the CUs (partial tiles and flags). A DEQUANT workspace must be zero-filled before its first use
- *            and used by one stream at a time; calls leave it ready for the next call.
+ *            activations); optional for IDOLQ_MODE_DEQUANT with tiled weights, where it lets the k stages of the
+ *            tiles left after whole rounds of the CUs be split over the CUs (tile counters, then partial tiles). A
+ *            DEQUANT workspace must be zero-filled before its first use and used by one stream at a time; calls
+ *            leave its counters at zero, ready for the next call.
  * Replaces src/kernels.hpp:73-76 gemm_packed (fp32 x, residual before GELU, column window n_offset / n) and
  * tools/idol_triton.py:94-126 fused_linear (bf16/fp16 x, bias after rounding: IDOLQ_FLAG_ROUND_BEFORE_BIAS). */
 int idolq_q8_0_gemm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* w, int64_t n_total,
@@ -76,7 +77,8 @@ int idolq_q8_0_gemm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ld
                     void* workspace, size_t workspace_bytes, void* stream);
 
 /* Workspace bytes idolq_q8_0_gemm uses for m rows of depth k in the given mode: the quantized activations for
- * IDOLQ_MODE_INT8, the partial tiles of the current device's CUs for IDOLQ_MODE_DEQUANT, 0 for IDOLQ_MODE_EXACT. */
+ * IDOLQ_MODE_INT8, the tile counters and partial tiles of the current device's CUs for IDOLQ_MODE_DEQUANT, 0 for
+ * IDOLQ_MODE_EXACT. */
 size_t idolq_q8_0_gemm_workspace(int64_t m, int64_t k, int mode);
 
 /* Quantizes an fp32 [n x k] matrix (row stride ldw) to Q8_0 blocks: per 32 values d = amax / 127,
@@ -84,12 +86,14 @@ size_t idolq_q8_0_gemm_workspace(int64_t m, int64_t k, int mode);
  * gguf-py's quantize(..., Q8_0) restates (tools/export_full_gguf.py:332-335, tests/python/test_fused_packed.py:40). */
 int idolq_q8_0_quantize(const float* w, int64_t n, int64_t k, int64_t ldw, uint8_t* out, void* stream);
 
-/* Tiled Q8_0: the same 34-byte blocks, reordered once (at load time) so that the bytes one GEMM stage reads are
- * contiguous. Rows are grouped in tiles of 128 (the last tile padded with zero blocks) and k in stages of 64 (two
- * blocks); chunk (t, s) = the 68 bytes of stage s of each of the 128 rows of tile t, row after row (8704 bytes), at
- * byte (t * (k / 64) + s) * 8704. Needs k % 64 == 0 (else the size is 0 / EINVAL). Layout of this library only: the
- * reference keeps GGUF blocks row-major (tools/idol_packed.py:28-31) and its CPU kernels use 16-column panels
- * (src/kernels.hpp:33-51). */
+/* Tiled (grouped) Q8_0: the same 34-byte blocks, reordered once (at load time) so that each GEMM load reads contiguous
+ * bytes already in MFMA operand order. Rows are grouped by 32 (the last group padded with zero rows) and k in stages
+ * of 64 (two blocks); chunk (g, s) of 2176 bytes at byte (g * (k / 64) + s) * 2176 holds, for b = 0, 1, the 32 codes
+ * of block 2 s + b of each row at [1024 b, 1024 b + 1024) -- lane l's 16 bytes at 16 l are codes 8 h .. 8 h + 7 then
+ * 16 + 8 h .. 16 + 8 h + 7 of row 32 g + l % 32, h = l / 32 -- and at [2048, 2176) per row r the fp16 scales of blocks
+ * 2 s (low half) and 2 s + 1 (high half) at 2048 + 4 r. Size = 34 bytes per 32 weights of the padded rows. Needs
+ * k % 64 == 0 (else the size is 0 / EINVAL). Layout of this library only: the reference keeps GGUF blocks row-major
+ * (tools/idol_packed.py:28-31) and its CPU kernels use 16-column panels (src/kernels.hpp:33-51). */
 int64_t idolq_q8_0_tiled_bytes(int64_t n, int64_t k);
 int idolq_q8_0_tile(const uint8_t* w, int64_t n, int64_t k, uint8_t* out, void* stream);
 

@@ -190,41 +190,57 @@ def test_empty_and_tiny_inputs():
     assert norm_rel(y, ref) < 1e-3 and abs(float(y[0, 0] - ref[0, 0])) <= terms * 2.0 ** -16
 
 
-@pytest.mark.parametrize("m,n,k", [(1024, 1536, 2048), (512, 384, 1280), (4096, 1536, 6144), (300, 520, 3072)])
+@pytest.mark.parametrize("m,n,k", [(1024, 1536, 2048), (512, 384, 1280), (4096, 1536, 6144), (300, 520, 3072),
+                                   (4096, 6144, 1536), (1000, 1536, 1536)])
 def test_split_k_matches_whole_tiles(m, n, k):
-    # DEQUANT with the k stages of the tiles split over the CUs (partial tiles summed through the workspace) against
-    # whole tiles per workgroup: the same products summed in another order (fp32), so within 1e-5 norm-relative before
-    # the bf16 output rounding; both within 1e-3 of an fp32 product of the dequantized weights. Three calls in a row
-    # give identical results (the workspace flags carry over between calls).
+    # DEQUANT on tiled weights with the k stages of the leftover tiles split over the CUs (stream-K: partial tiles
+    # added through the workspace) against whole tiles per workgroup: the same products summed in another grouping
+    # (fp32), so within 1e-5 norm-relative before the output rounding (fp32 output here); both within 1e-3 of an fp32
+    # product of the dequantized weights. Repeated calls agree to 1e-6 (the part that finishes a tile depends on
+    # timing), and every tile counter in the workspace is back to zero afterwards.
     rng = np.random.default_rng(m + n + k)
-    w = to_dev(q8(rng, n, k))
+    wq = to_dev(q8(rng, n, k))
+    w = L.tile_q8_0(wq, n, k)
     x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(DEV).bfloat16()
     b = torch.from_numpy(rng.normal(0, 0.01, n).astype(np.float32)).to(DEV)
-    whole = L.gemm(x, w, n, bias=b, mode=L.MODE_DEQUANT, out_dtype=torch.float32, split=False)
-    runs = [L.gemm(x, w, n, bias=b, mode=L.MODE_DEQUANT, out_dtype=torch.float32, split=True) for _ in range(3)]
+    whole = L.gemm(x, w, n, bias=b, mode=L.MODE_DEQUANT, out_dtype=torch.float32, split=False, tiled=True)
+    runs = [L.gemm(x, w, n, bias=b, mode=L.MODE_DEQUANT, out_dtype=torch.float32, split=True, tiled=True)
+            for _ in range(3)]
+    bf = [L.gemm(x, w, n, bias=b, residual=x[:, :n] if n <= k else None, mode=L.MODE_DEQUANT, split=s, tiled=True)
+          for s in (False, True)]
     torch.cuda.synchronize()
-    assert torch.equal(runs[0], runs[1]) and torch.equal(runs[1], runs[2])
+    assert norm_rel(runs[1].cpu().numpy(), runs[0].cpu().numpy()) < 1e-6
+    assert norm_rel(runs[2].cpu().numpy(), runs[0].cpu().numpy()) < 1e-6
     assert norm_rel(runs[0].cpu().numpy(), whole.cpu().numpy()) < 1e-5
-    ref = x.float() @ L.dequant(w, n, k, torch.bfloat16).float().T + b
+    # bf16 output through the register epilogue: split and whole differ at most by the output rounding
+    assert norm_rel(bf[1].float().cpu().numpy(), bf[0].float().cpu().numpy()) < 1e-3
+    ref = x.float() @ L.dequant(wq, n, k, torch.bfloat16).float().T + b
     assert norm_rel(runs[0].cpu().numpy(), ref.cpu().numpy()) < 1e-3
     ws = L._split_workspaces[x.device]
-    nbytes = int(L.load().idolq_q8_0_gemm_workspace(m, k, L.MODE_DEQUANT))
-    assert int(ws[nbytes - 256:nbytes - 252].view(torch.int32).item()) == 0  # no wait gave up
+    assert int(ws[:4096].view(torch.int32).abs().sum().item()) == 0  # every split tile was finished
 
 
 def tiled_layout(blocks, n, k):
-    """The tiled Q8_0 layout restated in numpy: chunk (t, s) = 68 bytes of stage s of each of rows 128 t .. 128 t + 127
-    (zero rows past n), chunks tile-major."""
+    """The tiled (grouped) Q8_0 layout restated in numpy: rows in groups of 32 (zero rows past n), k in stages of 64;
+    chunk (g, s) = block 2s codes, block 2s+1 codes (each 64 lanes x 16 bytes: lane l holds codes 8h..8h+7 and
+    16+8h..16+8h+7 of row l % 32, h = l // 32), then the two fp16 scales of each of the 32 rows; chunks group-major."""
     S = k // 64
-    raw = blocks.reshape(n, S, 68)
-    nt = (n + 127) // 128
-    pad = np.zeros((nt * 128, S, 68), np.uint8)
-    pad[:n] = raw
-    return pad.reshape(nt, 128, S, 68).transpose(0, 2, 1, 3).reshape(-1)
+    G = (n + 31) // 32
+    pad = np.zeros((G * 32, S * 68), np.uint8)
+    pad[:n] = blocks.reshape(n, S * 68)
+    raw = pad.reshape(G, 32, S, 68)
+    parts = []
+    for q in (raw[..., 2:34], raw[..., 36:68]):
+        lanes = np.stack([np.concatenate([q[..., 8 * h:8 * h + 8], q[..., 16 + 8 * h:24 + 8 * h]], axis=-1)
+                          for h in (0, 1)], axis=1)  # (G, h, r, S, 16)
+        parts.append(lanes.transpose(0, 3, 1, 2, 4).reshape(G, S, 1024))
+    scales = np.concatenate([raw[..., 0:2], raw[..., 34:36]], axis=-1).transpose(0, 2, 1, 3).reshape(G, S, 128)
+    return np.concatenate(parts + [scales], axis=-1).reshape(-1)
 
 
 @pytest.mark.parametrize("m,n,k,off,cnt", [(256, 128, 64, 0, 128), (300, 200, 192, 128, 72), (1000, 1536, 1536, 0, 1536),
-                                         (513, 4608, 1280, 1536, 1536)])
+                                         (513, 4608, 1280, 1536, 1536), (512, 512, 256, 96, 256), (256, 512, 128, 0, 512),
+                                         (700, 2048, 384, 0, 2048), (256, 64, 128, 0, 64)])
 def test_tiled_weights_match_row_major(m, n, k, off, cnt):
     # the tiled layout is a pure reordering of the blocks (bit-exact against the numpy restatement), and the GEMM on it
     # gives bit-identical results to the GEMM on the row-major blocks (same kernel arithmetic)
@@ -241,4 +257,4 @@ def test_tiled_weights_match_row_major(m, n, k, off, cnt):
         til = L.gemm(x, wt, n, off, cnt, bias=b, residual=res, act=act, mode=L.MODE_DEQUANT, tiled=True)
         assert torch.equal(raw, til)
     with pytest.raises(ValueError):
-        L.gemm(x, wt, n, 64, 64, mode=L.MODE_DEQUANT, tiled=True)  # window not on a 128-row tile
+        L.gemm(x, wt, n, 16, 16, mode=L.MODE_DEQUANT, tiled=True)  # window not on a 32-row group
