@@ -117,6 +117,7 @@ __device__ __forceinline__ float apply_act(int act, float v) {
             return v * __builtin_amdgcn_rcpf(1.0f + e);
         }
         case IDOLQ_ACT_RELU: return v > 0.0f ? v : 0.0f;
+        case IDOLQ_ACT_SILU: return v / (1.0f + expf(-v));
         default: return v;
     }
 }

@@ -110,7 +110,7 @@ extern "C" int idolq_linear_f32(const void* x, int x_dtype, int64_t m, int64_t k
     if (n > kMaxOut || n * k > kMaxWeights)
         return fail(IDOLQ_ENOSUPPORT, "dense linear: n <= 32 and n * k <= 16384 (weights held in LDS)");
     if (ldx < k || ldy < n) return fail(IDOLQ_EINVAL, "row stride smaller than the row");
-    if (act < IDOLQ_ACT_NONE || act > IDOLQ_ACT_RELU) return fail(IDOLQ_EINVAL, "unknown activation");
+    if (act < IDOLQ_ACT_NONE || act > IDOLQ_ACT_SILU) return fail(IDOLQ_EINVAL, "unknown activation");
     if (m == 0) return IDOLQ_OK;
     if (!x || !w || !y) return fail(IDOLQ_EINVAL, "x, w and y must be non-null");
     const int64_t blocks = (m + kThreads - 1) / kThreads;

@@ -300,7 +300,7 @@ extern "C" int idolq_quantize_act_q8(const void* x, int x_dtype, int64_t m, int6
 extern "C" int idolq_activation(void* x, int dtype, int64_t count, int act, void* stream) {
     if (!x && count > 0) return fail(IDOLQ_EINVAL, "x must be non-null");
     if (!dtype_ok(dtype)) return fail(IDOLQ_EINVAL, "unknown dtype code");
-    if (act < IDOLQ_ACT_NONE || act > IDOLQ_ACT_RELU) return fail(IDOLQ_EINVAL, "unknown activation");
+    if (act < IDOLQ_ACT_NONE || act > IDOLQ_ACT_SILU) return fail(IDOLQ_EINVAL, "unknown activation");
     if (count <= 0 || act == IDOLQ_ACT_NONE) return IDOLQ_OK;
     hipLaunchKernelGGL(activation_kernel, dim3(grid_for(count)), dim3(256), 0, static_cast<hipStream_t>(stream), x,
                        dtype, count, act);

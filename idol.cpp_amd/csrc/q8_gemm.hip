@@ -800,7 +800,7 @@ extern "C" int idolq_q8_0_gemm(const void* x, int x_dtype, int64_t m, int64_t k,
     if (n_offset < 0 || n_offset + n > n_total) return fail(IDOLQ_EINVAL, "column window outside the weight rows");
     if (ldx < k || ldy < n || (residual && ldr < n)) return fail(IDOLQ_EINVAL, "row stride smaller than the row");
     if (m > INT32_MAX / 2 || n > INT32_MAX / 2 || k > INT32_MAX / 2) return fail(IDOLQ_EINVAL, "dimension too large");
-    if (act < IDOLQ_ACT_NONE || act > IDOLQ_ACT_RELU) return fail(IDOLQ_EINVAL, "unknown activation");
+    if (act < IDOLQ_ACT_NONE || act > IDOLQ_ACT_SILU) return fail(IDOLQ_EINVAL, "unknown activation");
     if (residual == y && residual && (residual_dtype != y_dtype || ldr != ldy))
         return fail(IDOLQ_EINVAL, "a residual that aliases y must have y's dtype and stride");
     if ((reinterpret_cast<uintptr_t>(w) & 1) != 0) return fail(IDOLQ_EINVAL, "Q8_0 weights must be 2-byte aligned");

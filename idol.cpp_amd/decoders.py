@@ -1,0 +1,244 @@
+"""idol::Decoders on MI355X: the octree decoder and the Gaussian decoder of the real Idol model (src/decoders.cpp,
+include/idol/decoders.hpp), loaded from the native export (manifest.txt + weights.bin) and run on the GPU.
+
+Every operator is a libidolq HIP kernel, on fp32 activations like the reference's CPU path:
+  linears       Q8_0 GEMM (quantized layers; EXACT mode, or INT8 when the reference would use its integer kernel)
+                or the dense fp32 GEMM in the reference's summation order (unquantized layers, asymmetric panels);
+                the reference's separate SiLU / tanh-GELU passes are fused into the GEMM epilogue (the same fp32
+                operations on the same values: bias, then residual, then the activation)
+  layer norm    fp64 statistics (src/decoders.cpp:23-42), adaLN shift/scale from the level MLP
+  rms_heads, add_gated, the level embedding, the position embedding   one kernel each
+  attention     the fp32 attention kernel (src/kernels.cpp:735-746 semantics)
+Buffers are allocated per call from PyTorch's caching allocator. Inputs and outputs are fp32 GPU tensors; numpy
+arrays are accepted and copied to the device.
+
+The order of operations follows src/decoders.cpp:232-316 step by step. Output tolerance against the reference's
+float kernel is the one its own decoder check uses (norm-relative 2e-5, tests/python/test_gguf_decoder.py:63-65).
+"""
+import numpy as np
+import torch
+
+import idol_export as E
+import idol_kernels as K
+import idolq_lib as L
+
+
+class _Attn:
+    __slots__ = ("q", "kv", "qkv", "out", "q_gamma", "k_gamma")
+
+
+class Decoders:
+    """The reference's idol::Decoders (include/idol/decoders.hpp:36-77) on one GPU.
+
+    Decoders(path) reads an export directory; Decoders(export) takes an already-read idol_export.Export. Raises
+    RuntimeError for a missing or malformed export, with the reference's messages."""
+
+    def __init__(self, source, device="cuda"):
+        ex = source if isinstance(source, E.Export) else E.read_export(source)
+        self.device = torch.device(device)
+        if not ex.decoders:
+            raise RuntimeError("this export is not a decoders export (tools/export_idol.py)")
+        cfg = ex.decoder_config
+        D, H4 = cfg.dim, 4 * cfg.dim
+        if (D <= 0 or cfg.heads <= 0 or D % cfg.heads != 0 or cfg.cond <= 0 or cfg.per_anchor <= 0
+                or cfg.oct_blocks < 0 or cfg.gs_blocks < 0):
+            raise RuntimeError("manifest.txt describes an invalid decoder configuration")
+        self.cfg, self.rep = cfg, ex.rep
+        dev = self.device
+
+        def linear(prefix, out, in_):
+            q = E.take_qtensor(ex, prefix + ".weight")
+            if q is not None:
+                if q.out != out or q.in_ != in_:
+                    raise RuntimeError(f"quantized tensor '{prefix}.weight' has the wrong shape")
+                b = E.take_tensor(ex, prefix + ".bias", out)
+                if q.kind == "q8_0":
+                    return K.q8_0_linear(q.blob, b.data, out, in_, device=dev)
+                return K.quantized_linear(q.blob, b.data, out, in_, q.bits, q.group, device=dev)
+            w = E.take_tensor(ex, prefix + ".weight", out * in_)
+            b = E.take_tensor(ex, prefix + ".bias", out)
+            return K.pack_linear(w.data, b.data, out, in_, device=dev)
+
+        def vec(name, count):
+            return torch.from_numpy(E.take_tensor(ex, name, count).data.copy()).to(dev)
+
+        def attn(p, cross):
+            a = _Attn()
+            a.q = a.kv = a.qkv = None
+            if cross:
+                a.q = linear(p + ".to_q", D, D)
+                a.kv = linear(p + ".to_kv", 2 * D, cfg.cond)
+            else:
+                a.qkv = linear(p + ".to_qkv", 3 * D, D)
+            a.out = linear(p + ".to_out", D, D)
+            a.q_gamma = vec(p + ".q_rms_norm.gamma", D)
+            a.k_gamma = vec(p + ".k_rms_norm.gamma", D)
+            return a
+
+        self.oct_in = linear("oct.in_proj", D, 3)
+        self.oct_input = linear("oct.input_layer", D, D)
+        self.oct_l1 = linear("oct.l_embedder.mlp.0", D, 256)
+        self.oct_l2 = linear("oct.l_embedder.mlp.2", D, D)
+        self.oct_ada = linear("oct.adaLN_modulation.1", 6 * D, D)
+        self.oct_out = linear("oct.out_proj", 8, D)
+        self.oct = []
+        for i in range(cfg.oct_blocks):
+            p = f"oct.blocks.{i}."
+            self.oct.append((attn(p + "cross_attn", True), linear(p + "mlp.mlp.0", H4, D), linear(p + "mlp.mlp.2", D, H4)))
+
+        outs = cfg.per_anchor * 15
+        self.gs_in = linear("gs.in_proj", D, 3)
+        self.gs_input = linear("gs.input_layer", D, D)
+        self.gs_out = linear("gs.out_proj", outs, D)
+        self.perturbation = vec("gs.points_offset_perturbation", cfg.per_anchor * 3)
+        self.base_offset_scale = float(E.take_tensor(ex, "gs.base_offset_scale", 1).data[0])
+        self.gs = []
+        for i in range(cfg.gs_blocks):
+            p = f"gs.blocks.{i}."
+            self_attn, cross_attn = attn(p + "self_attn", False), attn(p + "cross_attn", True)
+            g2, b2 = vec(p + "norm2.weight", D), vec(p + "norm2.bias", D)
+            self.gs.append((self_attn, cross_attn, g2, b2, linear(p + "mlp.mlp.0", H4, D), linear(p + "mlp.mlp.2", D, H4)))
+
+        # the embedders' frequency tables as the export holds them (PyTorch's float32 values)
+        self.oct_pos_freqs = vec("oct.pos_embedder.freqs", D // 3 // 2)
+        self.gs_pos_freqs = vec("gs.pos_embedder.freqs", D // 3 // 2)
+        self.level_freqs = vec("oct.l_embedder.freqs", 128)
+
+        layers = [self.oct_in, self.oct_input, self.oct_l1, self.oct_l2, self.oct_ada, self.oct_out, self.gs_in,
+                  self.gs_input, self.gs_out]
+        for a, f1, f2 in self.oct:
+            layers += [a.q, a.kv, a.out, f1, f2]
+        for sa, ca, _, _, f1, f2 in self.gs:
+            layers += [sa.qkv, sa.out, ca.q, ca.kv, ca.out, f1, f2]
+        self._weight_bytes = sum(layer.bytes() for layer in layers)
+
+    # ---------------------------------------------------------------------------------------------------- queries
+    def config(self):
+        return self.cfg
+
+    def weight_bytes(self):
+        """Bytes the layers hold on the device (weights as stored here plus padded biases)."""
+        return self._weight_bytes
+
+    # ---------------------------------------------------------------------------------------------------- helpers
+    def _f32(self, a, name):
+        t = torch.as_tensor(a) if not isinstance(a, torch.Tensor) else a
+        if t.dtype != torch.float32:
+            raise ValueError(f"{name} must be fp32")
+        return t.to(self.device).contiguous()
+
+    @staticmethod
+    def _linear(a, w, out, residual=None, act=L.ACT_NONE):
+        """out = act(a @ W^T + bias + residual): gemm_packed (src/kernels.hpp:73-76) with the activation fused."""
+        if w.q8 is None:
+            return L.gemm_f32(a, w.weight, bias=w.bias[:w.out], residual=residual, act=act, out=out)
+        mode = L.MODE_INT8 if K._use_int8() else L.MODE_EXACT
+        return L.gemm(a, w.q8, w.out, 0, w.out, bias=w.bias[:w.out], residual=residual, act=act, mode=mode, out=out)
+
+    def _embed_points(self, freqs, x, rows, lin_in, lin_input, X, H):
+        """X = input_layer(in_proj(x) + pos_embed(x)) (src/decoders.cpp:247-250 and 283-286)."""
+        D = self.cfg.dim
+        fd = freqs.numel()
+        if 6 * fd < D:
+            H[:, 6 * fd:].zero_()
+        L.pos_embed(x, freqs, H[:, :6 * fd], ldo=D)
+        self._linear(x, lin_in, X, residual=H)
+        self._linear(X, lin_input, H)
+        return H, X  # the reference swaps X and H
+
+    def _cross_attention(self, a, h, rows, cond, cond_rows, Q, KV, A):
+        """src/decoders.cpp:232-240."""
+        D, heads = self.cfg.dim, self.cfg.heads
+        hd = D // heads
+        self._linear(h, a.q, Q)
+        L.rms_heads(Q, heads, hd, a.q_gamma)
+        self._linear(cond, a.kv, KV)
+        L.rms_heads(KV, heads, hd, a.k_gamma)
+        K.attention(Q, rows, D, KV, KV[:, D:], cond_rows, 2 * D, heads, hd, A, D)
+
+    # ---------------------------------------------------------------------------------------------------- decoders
+    def octree_logits(self, x, rows, resolution, cond, cond_rows, out=None):
+        """Octree decoder (src/decoders.cpp:242-279): x [rows, 3] cell centres, resolution 2^level, cond
+        [cond_rows, cond]. Returns (or writes) out [rows, 8]."""
+        cfg = self.cfg
+        D, H4 = cfg.dim, 4 * cfg.dim
+        x = self._f32(x, "x")[:rows]
+        cond = self._f32(cond, "cond")[:cond_rows]
+        dev = self.device
+        if out is None:
+            out = torch.empty((rows, 8), device=dev, dtype=torch.float32)
+        if rows == 0:
+            return out
+        X = torch.empty((rows, D), device=dev)
+        H = torch.empty_like(X)
+        Q, A = torch.empty_like(X), torch.empty_like(X)
+        F = torch.empty((rows, H4), device=dev)
+        KV = torch.empty((cond_rows, 2 * D), device=dev)
+
+        X, H = self._embed_points(self.oct_pos_freqs, x, rows, self.oct_in, self.oct_input, X, H)
+
+        # the octree level, embedded and turned into the shared adaLN modulation
+        emb = L.level_embed(resolution, self.level_freqs).view(1, -1)
+        l1 = torch.empty((1, D), device=dev)
+        l2 = torch.empty((1, D), device=dev)
+        mod = torch.empty((1, 6 * D), device=dev)
+        self._linear(emb, self.oct_l1, l1, act=L.ACT_SILU)
+        self._linear(l1, self.oct_l2, l2, act=L.ACT_SILU)
+        self._linear(l2, self.oct_ada, mod)
+        m = mod.view(-1)
+        shift_a, scale_a, gate_a = m[0:D], m[D:2 * D], m[2 * D:3 * D]
+        shift_m, scale_m, gate_m = m[3 * D:4 * D], m[4 * D:5 * D], m[5 * D:6 * D]
+
+        for a, ff1, ff2 in self.oct:
+            L.layernorm(X, 1e-6, shift=shift_a, scale=scale_a, out=H)
+            self._cross_attention(a, H, rows, cond, cond_rows, Q, KV, A)
+            self._linear(A, a.out, H)
+            L.add_gated(X, H, gate_a)
+            L.layernorm(X, 1e-6, shift=shift_m, scale=scale_m, out=H)
+            self._linear(H, ff1, F, act=L.ACT_GELU_TANH)
+            self._linear(F, ff2, H)
+            L.add_gated(X, H, gate_m)
+        L.layernorm(X, 1e-5, out=H)
+        self._linear(H, self.oct_out, out)
+        return out
+
+    def gaussian_features(self, points, rows, cond, cond_rows, out=None):
+        """Gaussian decoder (src/decoders.cpp:281-316): points [rows, 3] anchors, cond [cond_rows, cond]. Returns (or
+        writes) out [rows, per_anchor * 15] raw values."""
+        cfg = self.cfg
+        D, H4, heads = cfg.dim, 4 * cfg.dim, cfg.heads
+        hd = D // heads
+        points = self._f32(points, "points")[:rows]
+        cond = self._f32(cond, "cond")[:cond_rows]
+        dev = self.device
+        if out is None:
+            out = torch.empty((rows, cfg.per_anchor * 15), device=dev, dtype=torch.float32)
+        if rows == 0:
+            return out
+        X = torch.empty((rows, D), device=dev)
+        H = torch.empty_like(X)
+        Q, A = torch.empty_like(X), torch.empty_like(X)
+        F = torch.empty((rows, H4), device=dev)
+        QKV = torch.empty((rows, 3 * D), device=dev)
+        KV = torch.empty((cond_rows, 2 * D), device=dev)
+
+        X, H = self._embed_points(self.gs_pos_freqs, points, rows, self.gs_in, self.gs_input, X, H)
+
+        for sa, ca, g2, b2, ff1, ff2 in self.gs:
+            L.layernorm(X, 1e-6, out=H)
+            self._linear(H, sa.qkv, QKV)
+            L.rms_heads(QKV, heads, hd, sa.q_gamma)
+            L.rms_heads(QKV[:, D:], heads, hd, sa.k_gamma)
+            K.attention(QKV, rows, 3 * D, QKV[:, D:], QKV[:, 2 * D:], rows, 3 * D, heads, hd, A, D)
+            self._linear(A, sa.out, X, residual=X)
+
+            L.layernorm(X, 1e-6, gamma=g2, beta=b2, out=H)
+            self._cross_attention(ca, H, rows, cond, cond_rows, Q, KV, A)
+            self._linear(A, ca.out, X, residual=X)
+
+            L.layernorm(X, 1e-6, out=H)
+            self._linear(H, ff1, F, act=L.ACT_GELU_TANH)
+            self._linear(F, ff2, X, residual=X)
+        L.layernorm(X, 1e-5, out=H)
+        self._linear(H, self.gs_out, out)
+        return out

@@ -11,7 +11,7 @@ import torch
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libidolq.so"
 
 F32, F16, BF16 = 0, 1, 2
-ACT_NONE, ACT_GELU_ERF, ACT_GELU_TANH, ACT_RELU = 0, 1, 2, 3
+ACT_NONE, ACT_GELU_ERF, ACT_GELU_TANH, ACT_RELU, ACT_SILU = 0, 1, 2, 3, 4
 MODE_AUTO, MODE_DEQUANT, MODE_EXACT, MODE_INT8 = 0, 1, 2, 3
 FLAG_ROUND_BEFORE_BIAS, FLAG_TILED_WEIGHTS = 1, 2
 EINVAL, ELAUNCH, ENOSUPPORT = -1, -2, -3
@@ -43,6 +43,10 @@ _SIGNATURES = {
     "idolq_activation": (_int, [_vp, _int, _i64, _int, _vp]),
     "idolq_pos_embed": (_int, [_vp, _i64, _vp, _i64, _vp, _int, _i64, _vp]),
     "idolq_copy2d": (_int, [_vp, _int, _i64, _vp, _int, _i64, _i64, _i64, _vp]),
+    "idolq_gemm_f32": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _int, _vp, _i64, _vp]),
+    "idolq_rms_heads": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _vp, _vp]),
+    "idolq_add_gated": (_int, [_vp, _int, _i64, _vp, _int, _i64, _i64, _i64, _vp, _vp]),
+    "idolq_level_embed": (_int, [ctypes.c_float, _vp, _i64, _vp, _vp]),
 }
 
 _lib = None
@@ -310,3 +314,63 @@ def copy2d(src, dst):
     _check(lib.idolq_copy2d(_ptr(src), _code(src), _row_stride(src), _ptr(dst), _code(dst), _row_stride(dst), rows,
                             cols, _stream(src.device)))
     return dst
+
+
+def gemm_f32(x, w, bias=None, residual=None, act=ACT_NONE, out=None):
+    """Dense fp32 y = act(x @ w^T + bias + residual) in the reference's summation order; residual may be out."""
+    lib = load()
+    dev = _require_cuda(x, w, bias, residual, out)
+    m, k = x.shape
+    n = w.shape[0]
+    for t, name in ((x, "x"), (w, "w"), (bias, "bias"), (residual, "residual"), (out, "out")):
+        if t is not None and t.dtype != torch.float32:
+            raise ValueError(f"gemm_f32: {name} must be fp32")
+    if w.dim() != 2 or w.shape[1] != k or not w.is_contiguous():
+        raise ValueError("w must be a contiguous fp32 [n, k] matrix")
+    if bias is not None and (bias.numel() != n or not bias.is_contiguous()):
+        raise ValueError("bias must be n contiguous fp32 values")
+    if out is None:
+        out = torch.empty((m, n), device=x.device, dtype=torch.float32)
+    if residual is not None and residual.shape != (m, n):
+        raise ValueError("residual must be [m, n]")
+    ldr = _row_stride(residual) if residual is not None else 0
+    _check(lib.idolq_gemm_f32(_ptr(x), m, k, _row_stride(x), _ptr(w), n, _ptr(bias), _ptr(residual), ldr, act,
+                              _ptr(out), _row_stride(out), _stream(dev)))
+    return out
+
+
+def rms_heads(x, heads, head_dim, gamma):
+    """In place: each head of each row of x [rows, >= heads * head_dim] scaled to norm sqrt(head_dim), times gamma."""
+    lib = load()
+    _require_cuda(x, gamma)
+    if gamma.dtype != torch.float32 or gamma.numel() != heads * head_dim or not gamma.is_contiguous():
+        raise ValueError("gamma must be heads * head_dim contiguous fp32 values")
+    _check(lib.idolq_rms_heads(_ptr(x), _code(x), x.shape[0], _row_stride(x), heads, head_dim, _ptr(gamma),
+                               _stream(x.device)))
+    return x
+
+
+def add_gated(x, h, gate):
+    """In place: x += h * gate (gate per column)."""
+    lib = load()
+    _require_cuda(x, h, gate)
+    if h.shape != x.shape:
+        raise ValueError("add_gated needs x and h of one shape")
+    if gate.dtype != torch.float32 or gate.numel() != x.shape[1] or not gate.is_contiguous():
+        raise ValueError("gate must be one contiguous fp32 value per column")
+    _check(lib.idolq_add_gated(_ptr(x), _code(x), _row_stride(x), _ptr(h), _code(h), _row_stride(h), x.shape[0],
+                               x.shape[1], _ptr(gate), _stream(x.device)))
+    return x
+
+
+def level_embed(resolution, freqs, out=None):
+    """[cos | sin] of ((resolution * freqs) * 2) * pi, fp32 [2 * len(freqs)]."""
+    lib = load()
+    _require_cuda(freqs, out)
+    if freqs.dtype != torch.float32 or not freqs.is_contiguous():
+        raise ValueError("freqs must be contiguous fp32")
+    half = freqs.numel()
+    if out is None:
+        out = torch.empty(2 * half, device=freqs.device, dtype=torch.float32)
+    _check(lib.idolq_level_embed(float(resolution), _ptr(freqs), half, _ptr(out), _stream(freqs.device)))
+    return out

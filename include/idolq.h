@@ -23,7 +23,10 @@ extern "C" {
 
 enum { IDOLQ_F32 = 0, IDOLQ_F16 = 1, IDOLQ_BF16 = 2 };
 
-enum { IDOLQ_ACT_NONE = 0, IDOLQ_ACT_GELU_ERF = 1, IDOLQ_ACT_GELU_TANH = 2, IDOLQ_ACT_RELU = 3 };
+/* Activations applied after bias and residual. GELU_ERF is the reference's fused epilogue (src/kernels.cpp:826-850),
+ * GELU_TANH its decoder MLP activation (src/decoders.cpp:55-71), SILU x / (1 + exp(-x)) its level-embedding MLP
+ * activation (src/decoders.cpp:88). */
+enum { IDOLQ_ACT_NONE = 0, IDOLQ_ACT_GELU_ERF = 1, IDOLQ_ACT_GELU_TANH = 2, IDOLQ_ACT_RELU = 3, IDOLQ_ACT_SILU = 4 };
 
 /* GEMM arithmetic.
  *   DEQUANT  weights dequantized to the activation's 16-bit type (bf16 or fp16 of fp32(d) * q) in LDS, MFMA with fp32
@@ -154,6 +157,29 @@ int idolq_linear_f32(const void* x, int x_dtype, int64_t m, int64_t k, int64_t l
 /* Copies a [rows x cols] block between dtypes and strides (a column slice of a wider row is a pointer offset). */
 int idolq_copy2d(const void* src, int src_dtype, int64_t lds, void* dst, int dst_dtype, int64_t ldd, int64_t rows,
                  int64_t cols, void* stream);
+
+/* ---- The real decoders' operators (src/decoders.cpp), fp32 surface, in the reference's operation order. ---- */
+
+/* Dense fp32 GEMM of any shape: y[m x n] = act(x[m x k] * w^T + bias + residual), w [n x k] row-major, bias NULL or
+ * [n], residual NULL or [m x n] with row stride ldr (it may be y itself, with ldr == ldy; y must not overlap x).
+ * Replaces the reference's gemm_packed on an unquantized PackedLinear (src/kernels.hpp:73-76,
+ * src/kernels.cpp:566-596): the depth summed in 32-deep FMA chains added left to right, then bias, residual and the
+ * activation (src/kernels.cpp:212-241), so the result is bit-identical to it. m < 65535 * 64. */
+int idolq_gemm_f32(const float* x, int64_t m, int64_t k, int64_t ldx, const float* w, int64_t n, const float* bias,
+                   const float* residual, int64_t ldr, int act, float* y, int64_t ldy, void* stream);
+
+/* In place, for each row (row stride ld) and head: p = p * (sqrt(head_dim) / max(|p|, 1e-12)) * gamma[head, :], |p|
+ * from the sum of squares taken in order (src/decoders.cpp:74-86 rms_heads). gamma fp32 [heads * head_dim]. */
+int idolq_rms_heads(void* x, int dtype, int64_t rows, int64_t ld, int64_t heads, int64_t head_dim, const float* gamma,
+                    void* stream);
+
+/* x[r, c] += h[r, c] * gate[c] for r < rows, c < dim, one FMA per element (src/decoders.cpp:45-52 add_gated). */
+int idolq_add_gated(void* x, int x_dtype, int64_t ldx, const void* h, int h_dtype, int64_t ldh, int64_t rows,
+                    int64_t dim, const float* gate, void* stream);
+
+/* The octree level embedding: out[i] = cos(((resolution * freqs[i]) * 2) * pi), out[half + i] = sin(same), fp32,
+ * out [2 * half] (src/decoders.cpp:262-266). */
+int idolq_level_embed(float resolution, const float* freqs, int64_t half, float* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -102,6 +102,20 @@ def ref_lib():
         lib.ref_exp256.argtypes = [_f32p, _i64, _f32p]
         lib.ref_gelu256.argtypes = [_f32p, _i64, _f32p]
         lib.ref_gelu_scalar.argtypes = [_f32p, _i64, _f32p]
+        lib.ref_last_error.restype = ctypes.c_char_p
+        lib.ref_set_quant_kernel.argtypes = [_int]
+        lib.ref_rms_heads.argtypes = [_f32p, _int, _int, _int, _int, _f32p]
+        lib.ref_add_gated.argtypes = [_f32p, _f32p, _int, _int, _f32p]
+        lib.ref_decoders_open.argtypes = [ctypes.c_char_p]
+        lib.ref_decoders_open.restype = _vp
+        lib.ref_decoders_close.argtypes = [_vp]
+        lib.ref_decoders_config.argtypes = [_vp, _i32p]
+        lib.ref_decoders_weight_bytes.argtypes = [_vp]
+        lib.ref_decoders_weight_bytes.restype = _i64
+        lib.ref_decoders_octree_logits.argtypes = [_vp, _f32p, _int, ctypes.c_float, _f32p, _int, _f32p]
+        lib.ref_decoders_octree_logits.restype = _int
+        lib.ref_decoders_gaussian_features.argtypes = [_vp, _f32p, _int, _f32p, _int, _f32p]
+        lib.ref_decoders_gaussian_features.restype = _int
         _ref = lib
     return _ref
 
@@ -372,3 +386,54 @@ def ref_gelu_scalar(x):
 def set_threads(n):
     """OpenMP threads for both libraries (read at the next parallel region)."""
     os.environ["OMP_NUM_THREADS"] = str(n)
+
+
+def ref_rms_heads(x, heads, head_dim, gamma):
+    """src/decoders.cpp:74-86 on a copy of x [rows, ld]."""
+    y = _f32(x).copy()
+    ref_lib().ref_rms_heads(y, y.shape[0], y.shape[1], heads, head_dim, _f32(gamma))
+    return y
+
+
+def ref_add_gated(x, h, gate):
+    """src/decoders.cpp:45-52 on a copy of x [rows, dim]."""
+    y = _f32(x).copy()
+    ref_lib().ref_add_gated(y, _f32(h), y.shape[0], y.shape[1], _f32(gate))
+    return y
+
+
+class RefDecoders:
+    """The reference's idol::Decoders (src/decoders.cpp) over an export directory, on the CPU."""
+
+    def __init__(self, path):
+        lib = ref_lib()
+        self._h = lib.ref_decoders_open(str(path).encode())
+        if not self._h:
+            raise RuntimeError(lib.ref_last_error().decode())
+        cfg = np.zeros(6, np.int32)
+        lib.ref_decoders_config(self._h, cfg)
+        self.dim, self.heads, self.oct_blocks, self.gs_blocks, self.cond, self.per_anchor = (int(v) for v in cfg)
+
+    def close(self):
+        if self._h:
+            ref_lib().ref_decoders_close(self._h)
+            self._h = None
+
+    __del__ = close
+
+    def weight_bytes(self):
+        return int(ref_lib().ref_decoders_weight_bytes(self._h))
+
+    def octree_logits(self, x, resolution, cond):
+        x, cond = _f32(x), _f32(cond)
+        out = np.empty((x.shape[0], 8), np.float32)
+        if ref_lib().ref_decoders_octree_logits(self._h, x, x.shape[0], resolution, cond, cond.shape[0], out):
+            raise RuntimeError(ref_lib().ref_last_error().decode())
+        return out
+
+    def gaussian_features(self, points, cond):
+        points, cond = _f32(points), _f32(cond)
+        out = np.empty((points.shape[0], self.per_anchor * 15), np.float32)
+        if ref_lib().ref_decoders_gaussian_features(self._h, points, points.shape[0], cond, cond.shape[0], out):
+            raise RuntimeError(ref_lib().ref_last_error().decode())
+        return out

@@ -9,19 +9,23 @@
 #include "decoders.cpp"
 
 #include <cstdint>
+#include <cstring>
 #include <exception>
+#include <string>
 #include <vector>
 
 namespace {
 
 thread_local int g_status = 0;
+thread_local std::string g_message;
 
 template <typename F>
 int guarded(F&& f) {
     try {
         f();
         return 0;
-    } catch (const std::exception&) {
+    } catch (const std::exception& e) {
+        g_message = e.what();
         return -1;
     }
 }
@@ -110,6 +114,42 @@ void ref_gelu256(const float* x, std::int64_t count, float* y) {
 }
 void ref_gelu_scalar(const float* x, std::int64_t count, float* y) {
     for (std::int64_t i = 0; i < count; ++i) y[i] = idol::detail::gelu_scalar(x[i]);
+}
+
+// set_quant_kernel: -1 decide from IDOL_QUANT_KERNEL and the CPU, 0 float kernel, 1 integer kernel.
+void ref_set_quant_kernel(int mode) { idol::detail::set_quant_kernel(mode); }
+
+// The message of the last exception a guarded call caught on this thread.
+const char* ref_last_error() { return g_message.c_str(); }
+
+// rms_heads and add_gated of src/decoders.cpp, in place.
+void ref_rms_heads(float* x, int rows, int ld, int heads, int hd, const float* gamma) {
+    idol::rms_heads(x, rows, ld, heads, hd, gamma);
+}
+void ref_add_gated(float* x, const float* h, int rows, int dim, const float* gate) {
+    idol::add_gated(x, h, rows, dim, gate);
+}
+
+// idol::Decoders over an export directory: open (NULL on failure, message in ref_last_error), query, run, close.
+void* ref_decoders_open(const char* dir) {
+    idol::Decoders* d = nullptr;
+    guarded([&] { d = new idol::Decoders(dir); });
+    return d;
+}
+void ref_decoders_close(void* d) { delete static_cast<idol::Decoders*>(d); }
+void ref_decoders_config(void* d, int* cfg) {
+    const idol::DecoderConfig& c = static_cast<idol::Decoders*>(d)->config();
+    const int v[6] = {c.dim, c.heads, c.oct_blocks, c.gs_blocks, c.cond, c.per_anchor};
+    std::memcpy(cfg, v, sizeof v);
+}
+std::int64_t ref_decoders_weight_bytes(void* d) { return (std::int64_t)static_cast<idol::Decoders*>(d)->weight_bytes(); }
+int ref_decoders_octree_logits(void* d, const float* x, int rows, float resolution, const float* cond, int cond_rows,
+                               float* out) {
+    return guarded([&] { static_cast<idol::Decoders*>(d)->octree_logits(x, rows, resolution, cond, cond_rows, out); });
+}
+int ref_decoders_gaussian_features(void* d, const float* points, int rows, const float* cond, int cond_rows,
+                                   float* out) {
+    return guarded([&] { static_cast<idol::Decoders*>(d)->gaussian_features(points, rows, cond, cond_rows, out); });
 }
 
 }  // extern "C"

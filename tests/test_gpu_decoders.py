@@ -1,0 +1,197 @@
+"""The real decoders on the GPU (src/decoders.cpp) against the reference's own outputs: the operators one by one
+(bit-exact where the arithmetic is the same sequence of fp32 operations), the small fixture export with every weight
+form, and a model-width export (dim 1024, 16 heads of 64) checked against the reference build when it is present.
+
+Tolerance for decoder outputs: norm-relative 2e-5 against the reference's float kernel, the bar of its own decoder
+check (tests/python/test_gguf_decoder.py:63-65, tools/idol_decode.cpp:55-68)."""
+import importlib.util
+
+import numpy as np
+import pytest
+import torch
+
+import idol_kernels as K
+import idolq_lib as L
+import oracle as O
+from conftest import GOLDEN, norm_rel
+from decoders import Decoders
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _t(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _needs_ref():
+    if not O.ref_available():
+        pytest.skip("reference build absent (make -C oracle ref)")
+
+
+# ------------------------------------------------------------------------------------------------ operators
+@pytest.mark.parametrize("m,n,k", [(1, 64, 256), (37, 64, 3), (29, 128, 16), (70, 48, 100), (130, 200, 64), (5, 8, 1024)])
+def test_gemm_f32_is_bit_identical_to_the_reference_dense_gemm(m, n, k):
+    _needs_ref()
+    rng = np.random.default_rng(m * 7 + n)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    w = (rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32)
+    b = rng.standard_normal(n).astype(np.float32)
+    res = rng.standard_normal((m, n)).astype(np.float32)
+    got = L.gemm_f32(_t(a), _t(w), bias=_t(b)).cpu().numpy()
+    assert np.array_equal(got, O.ref_gemm_dense(a, w, b))
+    # a residual aliasing the output (the Gaussian decoder's X = out(A) + X)
+    y = _t(res)
+    L.gemm_f32(_t(a), _t(w), bias=_t(b), residual=y, out=y)
+    assert np.array_equal(y.cpu().numpy(), O.ref_gemm_dense(a, w, b, residual=res))
+    # and the mathematics: fp64 brute force
+    ref64 = a.astype(np.float64) @ w.astype(np.float64).T + b
+    assert np.max(np.abs(got - ref64)) <= 1e-5 * max(1.0, np.max(np.abs(ref64)))
+
+
+def test_gemm_f32_strided_rows_and_silu():
+    rng = np.random.default_rng(1)
+    a = rng.standard_normal((33, 80)).astype(np.float32)
+    w = rng.standard_normal((40, 48)).astype(np.float32) * 0.2
+    at = _t(a)[:, 16:64]
+    got = L.gemm_f32(at, _t(w), act=L.ACT_SILU).cpu().numpy().astype(np.float64)
+    v = a[:, 16:64].astype(np.float64) @ w.astype(np.float64).T
+    assert np.max(np.abs(got - v / (1 + np.exp(-v)))) < 1e-5
+    with pytest.raises(ValueError):
+        L.gemm_f32(_t(a), _t(w))  # k mismatch
+
+
+def test_rms_heads_and_add_gated_match_the_reference():
+    _needs_ref()
+    rng = np.random.default_rng(2)
+    rows, heads, hd, ld = 45, 4, 64, 3 * 256
+    x = rng.standard_normal((rows, ld)).astype(np.float32)
+    x[3, 320:384] = 0.0  # a zero head: the 1e-12 floor
+    g = rng.uniform(0.5, 1.5, heads * hd).astype(np.float32)
+    xt = _t(x)
+    L.rms_heads(xt[:, 256:], heads, hd, _t(g))
+    want = x.copy()
+    want[:, 256:] = O.ref_rms_heads(x[:, 256:].copy(), heads, hd, g)[:, :ld - 256]
+    got = xt.cpu().numpy()
+    assert np.array_equal(got[:, :256], x[:, :256]) and np.array_equal(got[:, 512:], x[:, 512:])
+    assert np.max(np.abs(got - want)) <= 2e-7 * np.max(np.abs(want))
+    # unit-norm heads times sqrt(hd) * gamma
+    h = got[:, 256:512].reshape(rows, heads, hd) / g.reshape(heads, hd)
+    norms = np.linalg.norm(h.astype(np.float64), axis=2)
+    assert np.allclose(np.delete(norms, 3, axis=0), np.sqrt(hd), rtol=1e-5)
+    assert np.all(got[3, 256 + 64:256 + 128] == 0)
+
+    dim = 96
+    xa = rng.standard_normal((rows, dim)).astype(np.float32)
+    ha = rng.standard_normal((rows, dim)).astype(np.float32)
+    gate = rng.standard_normal(dim).astype(np.float32)
+    xt = _t(xa)
+    L.add_gated(xt, _t(ha), _t(gate))
+    assert np.array_equal(xt.cpu().numpy(), O.ref_add_gated(xa, ha, gate))
+
+
+def test_level_embedding_and_silu():
+    f = np.exp(-np.log(np.float32(1024)) * np.arange(128, dtype=np.float32) / 128, dtype=np.float32)
+    for res in (2.0, 32.0, 1024.0):
+        got = L.level_embed(res, _t(f)).cpu().numpy()
+        ang = ((np.float32(res) * f) * np.float32(2.0)) * np.float32(np.pi)
+        assert ang.dtype == np.float32
+        want = np.concatenate([np.cos(ang.astype(np.float64)), np.sin(ang.astype(np.float64))])
+        assert np.max(np.abs(got - want)) < 2e-6
+    x = np.linspace(-30, 30, 4099).astype(np.float32)
+    xt = _t(x)
+    L.activation(xt, L.ACT_SILU)
+    want = x.astype(np.float64) / (1 + np.exp(-x.astype(np.float64)))
+    assert np.max(np.abs(xt.cpu().numpy() - want) / np.maximum(np.abs(want), 1e-30)) < 2e-6
+
+
+# ------------------------------------------------------------------------------------------------ whole decoders
+def _run(dec, anchors, cond, resolution):
+    a, c = _t(anchors), _t(cond)
+    oct_ = dec.octree_logits(a, a.shape[0], resolution, c, c.shape[0]).cpu().numpy()
+    gs = dec.gaussian_features(a, a.shape[0], c, c.shape[0]).cpu().numpy()
+    return oct_, gs
+
+
+def test_small_export_matches_the_reference_decoders(golden):
+    g = golden("decoders_small")
+    dec = Decoders(GOLDEN / "decoders_small")
+    try:
+        K.set_quant_kernel(0)
+        oct_, gs = _run(dec, g["anchors"], g["cond"], float(g["resolution"]))
+        r_oct, r_gs = norm_rel(oct_, g["ref_oct"]), norm_rel(gs, g["ref_gs"])
+        print(f"float kernel: octree {r_oct:.3e} gaussian {r_gs:.3e}")
+        assert r_oct < 2e-5 and r_gs < 2e-5
+    finally:
+        K.set_quant_kernel(-1)
+    # fewer rows than the buffers hold, and no rows
+    o2 = dec.octree_logits(_t(g["anchors"]), 5, float(g["resolution"]), _t(g["cond"]), 29)
+    assert o2.shape == (5, 8)
+    assert dec.gaussian_features(_t(g["anchors"]), 0, _t(g["cond"]), 29).shape == (0, 60)
+
+
+def _make_decoders_module():
+    spec = importlib.util.spec_from_file_location("make_decoders", GOLDEN / "make_decoders.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_symmetric_export_matches_the_reference_integer_kernel(golden, tmp_path):
+    # the fixture's weights with every panel symmetric, rebuilt from the generator's seed; the reference's outputs
+    # on it with its float and its integer (AVX-VNNI) kernels are in the fixture
+    g = golden("decoders_small")
+    if "sym_gs_int8" not in g:
+        pytest.skip("the fixture was written on a CPU without AVX-VNNI")
+    md = _make_decoders_module()
+    md.build_export(tmp_path / "sym", md.CFG, 11, md.SYM_FORMS)
+    dec = Decoders(tmp_path / "sym")
+    try:
+        K.set_quant_kernel(0)
+        oct_, gs = _run(dec, g["anchors"], g["cond"], float(g["resolution"]))
+        f_oct, f_gs = norm_rel(oct_, g["sym_oct"]), norm_rel(gs, g["sym_gs"])
+        K.set_quant_kernel(1)
+        oct8, gs8 = _run(dec, g["anchors"], g["cond"], float(g["resolution"]))
+        i_oct, i_gs = norm_rel(oct8, g["sym_oct_int8"]), norm_rel(gs8, g["sym_gs_int8"])
+    finally:
+        K.set_quant_kernel(-1)
+    print(f"float kernel: octree {f_oct:.3e} gaussian {f_gs:.3e}; integer kernel: octree {i_oct:.3e} "
+          f"gaussian {i_gs:.3e}; integer vs float {norm_rel(gs8, g['sym_gs']):.3e}")
+    assert f_oct < 2e-5 and f_gs < 2e-5
+    # the integer kernels agree far more closely than either agrees with the float kernel (about 1e-2 here)
+    assert i_oct < 1e-4 and i_gs < 1e-4
+
+
+def test_model_width_export_matches_the_reference_decoders(tmp_path):
+    # dim 1024, 16 heads of 64, per_anchor 32: the real model's widths, one block of each decoder
+    _needs_ref()
+    md = _make_decoders_module()
+    import idol_export as E
+    cfg = E.DecoderConfig(dim=1024, heads=16, oct_blocks=1, gs_blocks=1, cond=16, per_anchor=32)
+    forms = {name: "q8" for name in (
+        "oct.input_layer", "oct.l_embedder.mlp.0", "oct.l_embedder.mlp.2", "oct.adaLN_modulation.1", "oct.out_proj",
+        "oct.blocks.0.cross_attn.to_q", "oct.blocks.0.cross_attn.to_out", "oct.blocks.0.mlp.mlp.0",
+        "oct.blocks.0.mlp.mlp.2", "gs.input_layer", "gs.out_proj", "gs.blocks.0.self_attn.to_qkv",
+        "gs.blocks.0.self_attn.to_out", "gs.blocks.0.cross_attn.to_q", "gs.blocks.0.cross_attn.to_out",
+        "gs.blocks.0.mlp.mlp.0", "gs.blocks.0.mlp.mlp.2")}
+    md.build_export(tmp_path / "wide", cfg, 21, forms)
+    rng = np.random.default_rng(22)
+    anchors = rng.uniform(0, 1, (96, 3)).astype(np.float32)
+    cond = rng.standard_normal((300, 16)).astype(np.float32)
+    ref = O.RefDecoders(tmp_path / "wide")
+    O.ref_lib().ref_set_quant_kernel(0)
+    try:
+        want_oct = ref.octree_logits(anchors, 64.0, cond)
+        want_gs = ref.gaussian_features(anchors, cond)
+    finally:
+        O.ref_lib().ref_set_quant_kernel(-1)
+        ref.close()
+    dec = Decoders(tmp_path / "wide")
+    K.set_quant_kernel(0)
+    try:
+        oct_, gs = _run(dec, anchors, cond, 64.0)
+    finally:
+        K.set_quant_kernel(-1)
+    r_oct, r_gs = norm_rel(oct_, want_oct), norm_rel(gs, want_gs)
+    print(f"dim 1024: octree {r_oct:.3e} gaussian {r_gs:.3e}")
+    assert r_oct < 2e-5 and r_gs < 2e-5

@@ -169,8 +169,6 @@ def test_quantized_linear_rejects_shapes_the_format_cannot_hold():
         K.quantized_linear(bytes(10), bias, 16, 64, 4, 48)
     with pytest.raises(ValueError, match="multiple of 32"):
         K.quantized_linear(bytes(10), bias, 16, 96, 4, 64)
-    with pytest.raises(NotImplementedError):
-        K.quantized_linear(bytes(K.quant_panel_bytes(64, 4, 32)), bias, 16, 64, 4, 32)
     assert K.quant_panel_bytes(1024, 8, 32) == 32 * 576 == O.panel_bytes(16, 1024)
 
 
