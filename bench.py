@@ -14,6 +14,9 @@ Also reported, in the same JSON line:
                  --traffic-probe run (profiles/q8_gemm_mlp_block_traffic.md), scaled by a copy kernel of known size
   pct_int8_peak  value as a fraction of the gfx950 dense int8 MFMA peak (5.0 POP/s), as the metric asks
   denoiser_step_ms  one full synthetic denoiser step (24 layers, batch 2 x 4096 tokens), unless --no-denoiser
+  decoders_*     the real model's octree and Gaussian decoders (dim 1024, 16 heads, 4 and 16 blocks, 32 Gaussians per
+                 anchor) on 1024 anchors and 8192 latent tokens, fp32 activations, the reference's float-kernel
+                 numerics, unless --no-decoders; with the reference's own decoders timed on the host beside them
   cpu_baseline   the reference's own CPU kernels (oracle/_ref, float kernel, all host cores) on the same MLP block
 """
 import argparse
@@ -48,6 +51,8 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-denoiser", action="store_true")
     p.add_argument("--no-decoder-mlp", action="store_true")
+    p.add_argument("--no-decoders", action="store_true",
+                   help="skip the real-size octree and Gaussian decoders (dim 1024, 16 heads, 4 + 16 blocks)")
     p.add_argument("--denoiser-layers", type=int, default=24)
     p.add_argument("--cpu-rows", type=int, default=1024, help="rows of the MLP block the CPU baseline runs")
     p.add_argument("--traffic-probe", action="store_true",
@@ -240,6 +245,113 @@ def run_decoder_mlp(args):
     return out, model
 
 
+DEC_ROWS, DEC_TOKENS, DEC_LEVEL = 1024, 8192, 8
+
+
+def _decoder_config(oct_blocks=4, gs_blocks=16):
+    import idol_export as E
+    return E.DecoderConfig(dim=1024, heads=16, oct_blocks=oct_blocks, gs_blocks=gs_blocks, cond=16, per_anchor=32)
+
+
+def decoder_flop(cfg, rows, tokens):
+    """FLOP of one octree_logits and one gaussian_features call (matrix products and attention only)."""
+    D, C, H4 = cfg.dim, cfg.cond, 4 * cfg.dim
+    kv = 2 * tokens * C * 2 * D
+    cross = 2 * rows * D * D * 2 + kv + 4 * rows * tokens * D  # q, out, kv, QK^T and PV
+    mlp = 2 * rows * D * H4 * 2
+    embed = 2 * rows * (3 * D + D * D)
+    oct_ = embed + cfg.oct_blocks * (cross + mlp) + 2 * rows * D * 8
+    self_attn = 2 * rows * D * 3 * D + 2 * rows * D * D + 4 * rows * rows * D
+    gs = embed + cfg.gs_blocks * (self_attn + cross + mlp) + 2 * rows * D * cfg.per_anchor * 15
+    return oct_, gs
+
+
+def run_decoders(args):
+    """The real decoders at the model's size on 1024 anchors and 8192 latent tokens: median ms of 5 calls after a
+    warm-up, with the reference's float-kernel numerics (EXACT Q8_0 GEMMs, fp32 attention)."""
+    import torch
+    import idol_kernels as K
+    from decoders import Decoders, synthetic_export
+
+    cfg = _decoder_config()
+    dec = Decoders(synthetic_export(cfg, seed=0))
+    gen = torch.Generator().manual_seed(1)
+    anchors = torch.rand(DEC_ROWS, 3, generator=gen).cuda()
+    cond = torch.randn(DEC_TOKENS, cfg.cond, generator=gen).cuda()
+    res = float(1 << DEC_LEVEL)
+    K.set_quant_kernel(0)
+    out = {}
+    try:
+        for name, fn in (("oct", lambda: dec.octree_logits(anchors, DEC_ROWS, res, cond, DEC_TOKENS)),
+                         ("gs", lambda: dec.gaussian_features(anchors, DEC_ROWS, cond, DEC_TOKENS))):
+            fn()
+            torch.cuda.synchronize()
+            times = []
+            for _ in range(5):
+                t0 = time.perf_counter()
+                fn()
+                torch.cuda.synchronize()
+                times.append(time.perf_counter() - t0)
+            out[name] = sorted(times)[2] * 1e3
+    finally:
+        K.set_quant_kernel(-1)
+    f_oct, f_gs = decoder_flop(cfg, DEC_ROWS, DEC_TOKENS)
+    return {"decoders_oct_ms": round(out["oct"], 3), "decoders_gs_ms": round(out["gs"], 3),
+            "decoders_tflops": round((f_oct + f_gs) / ((out["oct"] + out["gs"]) * 1e-3) / 1e12, 2),
+            "decoders_config": f"dim 1024, 16 heads, 4 octree + 16 Gaussian blocks, 32 per anchor; {DEC_ROWS} anchors, "
+                               f"{DEC_TOKENS} latent tokens, fp32, float-kernel numerics"}
+
+
+def run_cpu_decoders():
+    """The reference's own idol::Decoders (oracle/_ref) on the host, same rows and tokens, all host cores. A bounded
+    sample: exports of the model's width with 1 and with 2 blocks per decoder are timed (median of 3 after a
+    warm-up); the per-block time is their difference, and the 4 + 16-block time is extrapolated from it."""
+    import tempfile
+    import numpy as np
+    import torch
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle as O
+    import idol_export as E
+    from decoders import synthetic_export
+
+    if not O.ref_available():
+        return {}
+    gen = torch.Generator().manual_seed(1)
+    anchors = torch.rand(DEC_ROWS, 3, generator=gen).numpy()
+    cond = torch.randn(DEC_TOKENS, 16, generator=gen).numpy()
+    res = float(1 << DEC_LEVEL)
+    times = {}
+    with tempfile.TemporaryDirectory(prefix="idolq-dec-") as tmp:
+        for nb in (1, 2):
+            ex = synthetic_export(_decoder_config(nb, nb), seed=0)
+            q = {name: E.QTensor(t.out, t.in_, 8, 32, O.q8_0_to_panel(t.blob.cpu().numpy(), t.out, t.in_))
+                 for name, t in ex.qtensors.items()}
+            dense = {name: t.data.reshape(t.shape) for name, t in ex.tensors.items()}
+            path = Path(tmp) / f"b{nb}"
+            E.write_export(path, ex.decoder_config, dense, q, rep=E.Representation())
+            del ex, q, dense
+            ref = O.RefDecoders(path)
+            O.ref_lib().ref_set_quant_kernel(0)
+            for name, fn in (("oct", lambda: ref.octree_logits(anchors, res, cond)),
+                             ("gs", lambda: ref.gaussian_features(anchors, cond))):
+                fn()
+                ts = []
+                for _ in range(3):
+                    t0 = time.perf_counter()
+                    fn()
+                    ts.append(time.perf_counter() - t0)
+                times[(name, nb)] = float(np.median(ts))
+            O.ref_lib().ref_set_quant_kernel(-1)
+            ref.close()
+    oct_s = times[("oct", 1)] + 3 * (times[("oct", 2)] - times[("oct", 1)])
+    gs_s = times[("gs", 1)] + 15 * (times[("gs", 2)] - times[("gs", 1)])
+    cores = int(os.environ.get("OMP_NUM_THREADS", 0)) or os.cpu_count()
+    return {"decoders_cpu_oct_ms_est": round(oct_s * 1e3, 1), "decoders_cpu_gs_ms_est": round(gs_s * 1e3, 1),
+            "decoders_cpu_cores": cores,
+            "decoders_cpu_note": "reference idol::Decoders, float kernel, model width with 1 and 2 blocks timed "
+                                 "(median of 3 after 1 warm-up), 4 + 16 blocks extrapolated from the per-block time"}
+
+
 def run_cpu_decoder_mlp(model, sample=16384):
     """The reference's CPU kernels (oracle/_ref: gemm_packed float kernel on the three Q8_0 layers, dense gemm_packed
     head; the position embedding from the oracle) on `sample` points, all host cores; scaled to 262144 points."""
@@ -399,6 +511,8 @@ def main():
     if not args.no_decoder_mlp:
         dec, dec_model = run_decoder_mlp(args)
         result.update(dec)
+    if not args.no_decoders:
+        result.update(run_decoders(args))
     model = ctx = None
     if not args.no_denoiser:
         dn, model, ctx = run_denoiser(args)
@@ -410,6 +524,13 @@ def main():
             result.update(cpu)
             if cpu:
                 result["denoiser_speedup_vs_cpu"] = round(cpu["denoiser_cpu_step_ms_est"] / result["denoiser_step_ms"], 1)
+        if not args.no_decoders:
+            cpu = run_cpu_decoders()
+            result.update(cpu)
+            if cpu:
+                result["decoders_speedup_vs_cpu"] = round(
+                    (cpu["decoders_cpu_oct_ms_est"] + cpu["decoders_cpu_gs_ms_est"])
+                    / (result["decoders_oct_ms"] + result["decoders_gs_ms"]), 1)
         if dec_model is not None:
             cpu = run_cpu_decoder_mlp(dec_model)
             result.update(cpu)

@@ -10,9 +10,12 @@
 // same fp16 values with dot2); the MFMA's k order is permuted to the order in which the score accumulator holds the
 // keys, and the V^T operand is read in that same order.
 //
+// attn_f32_mfma (fp32 inputs, head_dim 32 or 64, 16-byte aligned rows): fp32 matrix cores for both products, the key
+// range split over the 4 waves of a 32-query workgroup; the reference's float attention surface at fp32 accuracy.
+//
 // attn_f32 (any dtype, head_dim <= 256): one wave per (query, head, batch), 64 keys per step with one key per lane
-// for the scores and the head dimension split over lanes for P * V; fp32 throughout. Used for fp32 activations
-// (the reference's float attention surface) and head sizes other than 64.
+// for the scores and the head dimension split over lanes for P * V; fp32 throughout. Used for the remaining fp32
+// cases (unaligned rows, other head sizes) and 16-bit inputs with head sizes other than 64.
 #include "common.h"
 
 #include <type_traits>
@@ -290,6 +293,150 @@ __global__ __launch_bounds__(64) void attn_f32(AttnParams p) {
     }
 }
 
+// ------------------------------------------------------------------------------------------------ fp32 MFMA kernel
+// attn_f32_mfma<HD> (fp32 inputs, head_dim 32 or 64, 16-byte aligned rows): fp32 matrix cores
+// (v_mfma_f32_32x32x2_f32: fp32 products, fp32 accumulation) for both products, so the scores and the output keep
+// fp32 accuracy. A workgroup owns 32 queries of one (batch, head); its 4 waves split the key range into 4 contiguous
+// parts, each running an online softmax over 32-key tiles, and the four partial results (max, sum, unnormalized
+// output) are merged through LDS at the end.
+//   scores S^T = K Q^T: A = K tile (lane l: key l % 32), B = Q^T (lane l: query l % 32); the depth slot of lane l at
+//     step i is d = (l / 32) * HD / 2 + i, so each lane reads HD / 2 contiguous floats of its key and query rows.
+//     Accumulator element r of lane l is key 8 (r / 4) + 4 (l / 32) + r % 4 of query l % 32.
+//   output O^T += V^T P^T: step j takes the keys the lanes' accumulator element j holds (8 (j / 4) + 4 (l / 32) +
+//     j % 4), so P needs no exchange; A = V^T (lane l: d = l % 32 of the 32-wide d block).
+constexpr int kF32Waves = 4;
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_f32_mfma(AttnParams p) {
+    constexpr int HH = HD / 2;   // depth per lane half
+    constexpr int DB = HD / 32;  // 32-wide d blocks of the output
+    __shared__ float red_o[kF32Waves][HD][33];
+    __shared__ float red_m[kF32Waves][32], red_l[kF32Waves][32];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 31, half = lane >> 5;
+    const int64_t b = blockIdx.z, h = blockIdx.y;
+    const int64_t q0 = (int64_t)blockIdx.x * 32;
+    const int64_t lq = p.lq, lk = p.lk;
+    const float* qbase = static_cast<const float*>(p.q) + b * p.q_bs + h * HD;
+    const float* kbase = static_cast<const float*>(p.k) + b * p.kv_bs + h * HD;
+    const float* vbase = static_cast<const float*>(p.v) + b * p.kv_bs + h * HD;
+
+    float qv[HH];
+    {
+        const float* qr = qbase + (q0 + col < lq ? q0 + col : lq - 1) * p.ldq + half * HH;
+#pragma unroll
+        for (int i = 0; i < HH; i += 4) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(qr + i);
+            qv[i] = v[0], qv[i + 1] = v[1], qv[i + 2] = v[2], qv[i + 3] = v[3];
+        }
+    }
+
+    const int64_t tiles = (lk + 31) / 32, per = (tiles + kF32Waves - 1) / kF32Waves;
+    const int64_t t0 = wave * per, t1 = t0 + per < tiles ? t0 + per : tiles;
+    const float c = p.scale_log2;
+    float m = -INFINITY, l = 0.0f;
+    f32x16 o[DB];
+#pragma unroll
+    for (int t = 0; t < DB; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[t][r] = 0.0f;
+
+    // K and V of the next tile are loaded while the current one is multiplied (register double buffer)
+    float kn[HH], vn[DB][16];
+    auto load_tile = [&](int64_t k0) {
+        const float* kr = kbase + (k0 + col < lk ? k0 + col : lk - 1) * p.ldkv + half * HH;
+#pragma unroll
+        for (int i = 0; i < HH; i += 4) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(kr + i);
+            kn[i] = v[0], kn[i + 1] = v[1], kn[i + 2] = v[2], kn[i + 3] = v[3];
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int64_t key = k0 + 8 * (j >> 2) + 4 * half + (j & 3);
+            const float* vr = vbase + (key < lk ? key : lk - 1) * p.ldkv + col;
+#pragma unroll
+            for (int t2 = 0; t2 < DB; ++t2) vn[t2][j] = vr[t2 * 32];
+        }
+    };
+    if (t0 < t1) load_tile(t0 * 32);
+    for (int64_t t = t0; t < t1; ++t) {
+        const int64_t k0 = t * 32;
+        float kv[HH], vv[DB][16];
+#pragma unroll
+        for (int i = 0; i < HH; ++i) kv[i] = kn[i];
+#pragma unroll
+        for (int t2 = 0; t2 < DB; ++t2)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) vv[t2][j] = vn[t2][j];
+        if (t + 1 < t1) load_tile(k0 + 32);
+        f32x16 s;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < HH; ++i) s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[i], qv[i], s, 0, 0, 0);
+
+        float mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t key = k0 + 8 * (r >> 2) + 4 * half + (r & 3);
+            s[r] = key < lk ? s[r] * c : -INFINITY;
+            mx = fmaxf(mx, s[r]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m, mx);
+        const float alpha = exp2f(m - m_new);
+        float sum = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            s[r] = exp2f(s[r] - m_new);
+            sum += s[r];
+        }
+        l = l * alpha + sum;
+        m = m_new;
+#pragma unroll
+        for (int t2 = 0; t2 < DB; ++t2) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[t2][r] *= alpha;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) o[t2] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[t2][j], s[j], o[t2], 0, 0, 0);
+        }
+    }
+    l += __shfl_xor(l, 32);
+
+    // merge the waves' partial results: out = sum_w O_w 2^(m_w - m*) / sum_w l_w 2^(m_w - m*)
+#pragma unroll
+    for (int t2 = 0; t2 < DB; ++t2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red_o[wave][t2 * 32 + 8 * (r >> 2) + 4 * half + (r & 3)][col] = o[t2][r];
+    if (half == 0) {
+        red_m[wave][col] = m;
+        red_l[wave][col] = l;
+    }
+    __syncthreads();
+    const int qi = threadIdx.x >> 3, part = threadIdx.x & 7;  // 32 queries x 8 column parts
+    float mstar = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kF32Waves; ++w) mstar = fmaxf(mstar, red_m[w][qi]);
+    float wgt[kF32Waves], lsum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kF32Waves; ++w) {
+        wgt[w] = red_m[w][qi] == -INFINITY ? 0.0f : exp2f(red_m[w][qi] - mstar);
+        lsum += red_l[w][qi] * wgt[w];
+    }
+    const float inv = 1.0f / lsum;
+    if (q0 + qi < lq) {
+        const int64_t obase = b * p.o_bs + (q0 + qi) * p.ldo + h * HD;
+#pragma unroll
+        for (int d = part; d < HD; d += 8) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kF32Waves; ++w) acc += red_o[w][d][qi] * wgt[w];
+            store_from_float(p.out, p.out_dt, obase + d, acc * inv);
+        }
+    }
+}
+
 }  // namespace
 }  // namespace idolq
 
@@ -320,6 +467,14 @@ extern "C" int idolq_attention(const void* q, const void* k, const void* v, int 
         else
             hipLaunchKernelGGL(attn_mfma_hd64<_Float16>, grid, dim3(256), 0, s, p);
         return check_launch("attn_mfma_hd64");
+    }
+    if (dtype == IDOLQ_F32 && (head_dim == 32 || head_dim == 64) && aligned) {
+        const dim3 grid((unsigned)((lq + 31) / 32), (unsigned)heads, (unsigned)batch);
+        if (head_dim == 64)
+            hipLaunchKernelGGL(attn_f32_mfma<64>, grid, dim3(256), 0, s, p);
+        else
+            hipLaunchKernelGGL(attn_f32_mfma<32>, grid, dim3(256), 0, s, p);
+        return check_launch("attn_f32_mfma");
     }
     const dim3 grid((unsigned)lq, (unsigned)heads, (unsigned)batch);
     hipLaunchKernelGGL(attn_f32, grid, dim3(64), 0, s, p);

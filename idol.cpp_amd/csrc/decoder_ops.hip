@@ -26,6 +26,36 @@ __global__ __launch_bounds__(256) void rms_heads_kernel(void* x, int dt, int64_t
     for (int d = 0; d < hd; ++d) store_from_float(x, dt, base + d, load_as_float(x, dt, base + d) * mult * g[d]);
 }
 
+// The same for fp32 rows with 16-byte aligned heads of HD values: the head held in registers, read and written with
+// 16-byte accesses; the sum of squares is still taken in order, so the result is that of rms_heads_kernel.
+template <int HD>
+__global__ __launch_bounds__(256) void rms_heads_vec_kernel(float* x, int64_t rows, int64_t ld, int heads,
+                                                            const float* __restrict__ gamma) {
+    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= rows * heads) return;
+    const int64_t r = id / heads;
+    const int h = (int)(id - r * heads);
+    f32x4* p = reinterpret_cast<f32x4*>(x + r * ld + (int64_t)h * HD);
+    const f32x4* g = reinterpret_cast<const f32x4*>(gamma + (int64_t)h * HD);
+    f32x4 v[HD / 4];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < HD / 4; ++i) {
+        v[i] = p[i];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ss = fmaf(v[i][e], v[i][e], ss);
+    }
+    const float mult = sqrtf((float)HD) / fmaxf(sqrtf(ss), 1e-12f);
+#pragma unroll
+    for (int i = 0; i < HD / 4; ++i) {
+        const f32x4 gi = g[i];
+        f32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = v[i][e] * mult * gi[e];
+        p[i] = o;
+    }
+}
+
 // x[r, c] += h[r, c] * gate[c] (src/decoders.cpp:45-52 add_gated; the multiply-add is one FMA, as GCC contracts it).
 __global__ __launch_bounds__(256) void add_gated_kernel(void* x, int xdt, int64_t ldx, const void* h, int hdt,
                                                         int64_t ldh, int64_t rows, int64_t dim,
@@ -130,6 +160,17 @@ extern "C" int idolq_rms_heads(void* x, int dtype, int64_t rows, int64_t ld, int
         return fail(IDOLQ_EINVAL, "rms_heads: need rows >= 0, heads > 0, head_dim > 0 and ld >= heads * head_dim");
     if (rows == 0) return IDOLQ_OK;
     if (!x || !gamma) return fail(IDOLQ_EINVAL, "x and gamma must be non-null");
+    const bool al = reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(gamma) % 16 == 0 &&
+                    ld % 4 == 0;
+    if (dtype == IDOLQ_F32 && al && (head_dim == 32 || head_dim == 64 || head_dim == 128)) {
+        const dim3 grid((unsigned)((rows * heads + 255) / 256));
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        float* xf = static_cast<float*>(x);
+        if (head_dim == 32) hipLaunchKernelGGL(rms_heads_vec_kernel<32>, grid, dim3(256), 0, s, xf, rows, ld, (int)heads, gamma);
+        else if (head_dim == 64) hipLaunchKernelGGL(rms_heads_vec_kernel<64>, grid, dim3(256), 0, s, xf, rows, ld, (int)heads, gamma);
+        else hipLaunchKernelGGL(rms_heads_vec_kernel<128>, grid, dim3(256), 0, s, xf, rows, ld, (int)heads, gamma);
+        return check_launch("rms_heads_vec_kernel");
+    }
     hipLaunchKernelGGL(rms_heads_kernel, dim3((unsigned)((rows * heads + 255) / 256)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), x, dtype, rows, ld, (int)heads, (int)head_dim, gamma);
     return check_launch("rms_heads_kernel");

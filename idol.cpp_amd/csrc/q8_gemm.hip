@@ -740,10 +740,11 @@ TileChoice choose_tile(int m, int n, const TileChoice* cands, int count) {
 
 int launch_16bit(GemmParams p, int xt, int mode, bool w4, void* workspace, size_t workspace_bytes, hipStream_t stream) {
     if (xt == XT_F32) {
-        static const TileChoice cands[] = {{128, 128, 1.0f}, {128, 64, 1.0f}};
-        const TileChoice t = choose_tile(p.m, p.n, cands, 2);
+        static const TileChoice cands[] = {{128, 128, 1.0f}, {128, 64, 1.0f}, {64, 64, 0.75f}};
+        const TileChoice t = choose_tile(p.m, p.n, cands, 3);
         if (t.bn == 128) return launch_f32_tile<128, 128>(p, w4, stream);
-        return launch_f32_tile<128, 64>(p, w4, stream);
+        if (t.bm == 128) return launch_f32_tile<128, 64>(p, w4, stream);
+        return launch_f32_tile<64, 64>(p, w4, stream);
     }
     static const TileChoice cands[] = {{256, 128, 1.0f}, {128, 128, 0.5f}, {128, 64, 0.6f}};
     const TileChoice t = choose_tile(p.m, p.n, cands, 3);

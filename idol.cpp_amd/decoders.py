@@ -242,3 +242,67 @@ class Decoders:
         L.layernorm(X, 1e-5, out=H)
         self._linear(H, self.gs_out, out)
         return out
+
+
+def synthetic_export(cfg, seed=0, device="cuda"):
+    """An in-memory export of randomly initialised decoders with the weight forms of the real model's GGUF export:
+    every matrix whose input width is a multiple of 256 as Q8_0 blocks (quantized on the GPU), the k = 3 input
+    projections and the k = cond latent projections as fp32 (tools/export_full_gguf.py:91 quantizes only those).
+    Weights ~ N(0, 1/in), biases ~ N(0, 0.02^2), norm and RMS gains ~ 1 + N(0, 0.1^2). For benchmarks."""
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    D, C = cfg.dim, cfg.cond
+    ex = E.Export(decoders=True, decoder_config=cfg)
+
+    def randn(*shape):
+        return torch.randn(*shape, generator=gen, dtype=torch.float32)
+
+    def linear(prefix, out, in_):
+        w = randn(out, in_) / float(np.sqrt(in_))
+        if in_ % 256 == 0:
+            ex.qtensors[prefix + ".weight"] = E.QTensor(out, in_, 8, 32, L.quantize_q8_0(w.to(device)), kind="q8_0")
+        else:
+            ex.tensors[prefix + ".weight"] = E.Tensor([out, in_], w.numpy().reshape(-1))
+        ex.tensors[prefix + ".bias"] = E.Tensor([out], (0.02 * randn(out)).numpy())
+
+    def vec(name, values):
+        ex.tensors[name] = E.Tensor([values.size], np.ascontiguousarray(values, np.float32).reshape(-1))
+
+    def attn(p, cross):
+        if cross:
+            linear(p + ".to_q", D, D)
+            linear(p + ".to_kv", 2 * D, C)
+        else:
+            linear(p + ".to_qkv", 3 * D, D)
+        linear(p + ".to_out", D, D)
+        vec(p + ".q_rms_norm.gamma", (1 + 0.1 * randn(D)).numpy())
+        vec(p + ".k_rms_norm.gamma", (1 + 0.1 * randn(D)).numpy())
+
+    linear("oct.in_proj", D, 3)
+    linear("oct.input_layer", D, D)
+    linear("oct.l_embedder.mlp.0", D, 256)
+    linear("oct.l_embedder.mlp.2", D, D)
+    linear("oct.adaLN_modulation.1", 6 * D, D)
+    linear("oct.out_proj", 8, D)
+    for i in range(cfg.oct_blocks):
+        attn(f"oct.blocks.{i}.cross_attn", True)
+        linear(f"oct.blocks.{i}.mlp.mlp.0", 4 * D, D)
+        linear(f"oct.blocks.{i}.mlp.mlp.2", D, 4 * D)
+    linear("gs.in_proj", D, 3)
+    linear("gs.input_layer", D, D)
+    linear("gs.out_proj", cfg.per_anchor * 15, D)
+    vec("gs.points_offset_perturbation", (0.1 * randn(cfg.per_anchor * 3)).numpy())
+    vec("gs.base_offset_scale", np.array([0.5], np.float32))
+    for i in range(cfg.gs_blocks):
+        p = f"gs.blocks.{i}."
+        attn(p + "self_attn", False)
+        attn(p + "cross_attn", True)
+        vec(p + "norm2.weight", (1 + 0.1 * randn(D)).numpy())
+        vec(p + "norm2.bias", (0.05 * randn(D)).numpy())
+        linear(p + "mlp.mlp.0", 4 * D, D)
+        linear(p + "mlp.mlp.2", D, 4 * D)
+    fd = D // 3 // 2
+    freqs = torch.pow(2.0, torch.linspace(0.0, 10.0, fd, dtype=torch.float32)).numpy()
+    vec("oct.pos_embedder.freqs", freqs)
+    vec("gs.pos_embedder.freqs", freqs)
+    vec("oct.l_embedder.freqs", torch.exp(-np.log(1024) * torch.arange(0, 128, dtype=torch.float32) / 128).numpy())
+    return ex

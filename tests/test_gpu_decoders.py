@@ -80,6 +80,16 @@ def test_rms_heads_and_add_gated_match_the_reference():
     norms = np.linalg.norm(h.astype(np.float64), axis=2)
     assert np.allclose(np.delete(norms, 3, axis=0), np.sqrt(hd), rtol=1e-5)
     assert np.all(got[3, 256 + 64:256 + 128] == 0)
+    # a head size the 16-byte kernel does not take (general kernel), and bf16 rows
+    x48 = rng.standard_normal((7, 3 * 48)).astype(np.float32)
+    g48 = rng.uniform(0.5, 1.5, 3 * 48).astype(np.float32)
+    xt = _t(x48)
+    L.rms_heads(xt, 3, 48, _t(g48))
+    assert np.max(np.abs(xt.cpu().numpy() - O.ref_rms_heads(x48, 3, 48, g48))) <= 2e-7 * 8
+    xb = _t(x48).bfloat16()
+    want_b = O.ref_rms_heads(xb.float().cpu().numpy(), 3, 48, g48)
+    L.rms_heads(xb, 3, 48, _t(g48))
+    assert np.max(np.abs(xb.float().cpu().numpy() - want_b)) <= 2e-2
 
     dim = 96
     xa = rng.standard_normal((rows, dim)).astype(np.float32)

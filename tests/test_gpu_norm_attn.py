@@ -151,3 +151,34 @@ def test_activations_and_position_embedding(golden):
     ref = O.pos_embed(freqs, coords)
     got = out.cpu().numpy()
     assert np.max(np.abs(got[:, 256:] - ref)) < 1e-4 and not got[:, :256].any()
+
+
+@pytest.mark.parametrize("hd", [32, 64])
+@pytest.mark.parametrize("lq,lk,heads,batch", [(1, 1, 1, 1), (37, 29, 2, 1), (130, 77, 2, 2), (64, 1000, 3, 1),
+                                               (300, 64, 1, 1), (33, 4133, 2, 1)])
+def test_attention_fp32_matrix_cores_match_the_reference(hd, lq, lk, heads, batch):
+    # fp32 inputs with 16-byte aligned rows and head_dim 32 / 64 take the fp32 matrix-core kernel: fp32 products and
+    # sums, so it tracks the reference's fp32 attention as closely as its fp32 kernel does (1e-5 bar, usually ~1e-7);
+    # q, k and v are views into one projection buffer, with a batch stride
+    rng = np.random.default_rng(lq * 31 + lk + hd)
+    dim = heads * hd
+    qkv = rng.normal(0, 1, (batch, max(lq, lk), 3 * dim)).astype(np.float32)
+    buf = to_dev(qkv)
+    bs = max(lq, lk) * 3 * dim
+    out = torch.full((batch, lq, dim + 4), float("nan"), device=DEV)
+    L.attention(buf[:, :, :dim], buf[:, :, dim:2 * dim], buf[:, :, 2 * dim:], batch, lq, lk, heads, hd, 3 * dim,
+                3 * dim, bs, bs, out, dim + 4, lq * (dim + 4))
+    got = out.cpu().numpy()
+    assert np.all(np.isnan(got[:, :, dim:]))  # nothing written past the row
+    for bi in range(batch):
+        blk = qkv[bi]
+        q, k, v = blk[:lq, :dim], blk[:lk, dim:2 * dim], blk[:lk, 2 * dim:]
+        want = O.attention(q, k, v, lq, lk, dim, dim, heads, hd)
+        assert norm_rel(got[bi, :, :dim], want) < 1e-5
+        if O.ref_available():
+            assert norm_rel(got[bi, :, :dim], O.ref_attention(q, k, v, lq, lk, dim, dim, heads, hd)) < 1e-5
+        # fp64 softmax attention, one head
+        s = q[:, :hd].astype(np.float64) @ k[:, :hd].astype(np.float64).T / np.sqrt(hd)
+        pr = np.exp(s - s.max(axis=1, keepdims=True))
+        o64 = (pr / pr.sum(axis=1, keepdims=True)) @ v[:, :hd].astype(np.float64)
+        assert np.max(np.abs(got[bi, :, :hd] - o64)) < 2e-5
