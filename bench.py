@@ -14,6 +14,7 @@ Also reported, in the same JSON line:
                  --traffic-probe run (profiles/q8_gemm_mlp_block_traffic.md), scaled by a copy kernel of known size
   pct_int8_peak  value as a fraction of the gfx950 dense int8 MFMA peak (5.0 POP/s), as the metric asks
   denoiser_step_ms  one full synthetic denoiser step (24 layers, batch 2 x 4096 tokens), unless --no-denoiser
+  fused_*        fused_linear per fused kind (Q8_0, Q4_0, Q4_K) at the up-projection shape, with bias
   decoders_*     the real model's octree and Gaussian decoders (dim 1024, 16 heads, 4 and 16 blocks, 32 Gaussians per
                  anchor) on 1024 anchors and 8192 latent tokens, fp32 activations, the reference's float-kernel
                  numerics, unless --no-decoders; with the reference's own decoders timed on the host beside them
@@ -302,6 +303,45 @@ def run_decoders(args):
                                f"{DEC_TOKENS} latent tokens, fp32, float-kernel numerics"}
 
 
+def run_fused_kinds(args):
+    """fused_linear (the packed-linear surface) for each fused kind at the MLP block's up-projection shape, bf16
+    x [4096, 1536] -> [4096, 6144] with bias: ms per call (20 calls after 3 warm-ups) and TFLOP/s."""
+    import numpy as np
+    import torch
+    import idolq_lib as L
+    from idol_hip import fused_linear
+
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    x = torch.randn(M, D, device="cuda", dtype=torch.bfloat16, generator=gen)
+    bias = (0.01 * torch.randn(H, device="cuda", generator=gen)).bfloat16()
+    w = 0.02 * torch.randn(H, D, device="cuda", generator=gen)
+    q8 = L.quantize_q8_0(w)
+    rng = np.random.default_rng(4)
+    q4k = rng.integers(0, 256, size=(H * D // 256, 144), dtype=np.uint8)
+    q4k[:, :4] = np.frombuffer(np.array([0.001, 0.0005], np.float16).tobytes(), np.uint8)
+    # Q4_0 blocks of the same weights: scale = max-magnitude value / -8, codes clipped to 0..15 (ggml's rule)
+    g = w.reshape(-1, 32)
+    m = g.gather(1, g.abs().argmax(1, keepdim=True))
+    d = (m / -8.0).half()
+    inv = torch.where(d != 0, 1.0 / d.float(), torch.zeros_like(d, dtype=torch.float32))
+    q = torch.clamp(torch.trunc(g * inv + 8.5), max=15).to(torch.uint8)
+    q4 = torch.cat([d.view(torch.uint8).reshape(-1, 2), q[:, :16] | (q[:, 16:] << 4)], dim=1).reshape(-1)
+    out = {}
+    for name, code, packed in (("q8_0", 8, q8), ("q4_0", 4, q4), ("q4_k", 44, torch.from_numpy(q4k).cuda().reshape(-1))):
+        with torch.no_grad():
+            for _ in range(3):
+                fused_linear(x, packed, (H, D), code, bias)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(20):
+                fused_linear(x, packed, (H, D), code, bias)
+            torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) / 20 * 1e3
+        out[f"fused_{name}_ms"] = round(ms, 4)
+        out[f"fused_{name}_tflops"] = round(2.0 * M * D * H / (ms * 1e-3) / 1e12, 1)
+    return out
+
+
 def run_cpu_decoders():
     """The reference's own idol::Decoders (oracle/_ref) on the host, same rows and tokens, all host cores. A bounded
     sample: exports of the model's width with 1 and with 2 blocks per decoder are timed (median of 3 after a
@@ -511,6 +551,7 @@ def main():
     if not args.no_decoder_mlp:
         dec, dec_model = run_decoder_mlp(args)
         result.update(dec)
+    result.update(run_fused_kinds(args))
     if not args.no_decoders:
         result.update(run_decoders(args))
     model = ctx = None

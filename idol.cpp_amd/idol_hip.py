@@ -1,9 +1,15 @@
-"""Fused Q8_0 linear on MI355X: the drop-in for the reference's tools/idol_triton.py:fused_linear.
+"""Fused packed linear on MI355X: the drop-in for the reference's tools/idol_triton.py:fused_linear.
 
 fused_linear keeps the reference's signature, validation and error messages (tools/idol_triton.py:94-111) and its
-numerics: weights dequantized to the activation dtype (fp32(d) * q, rounded), fp32 accumulation, the product
-rounded to the output dtype before the bias is added (tools/idol_triton.py:84-89). The arithmetic runs in
-libidolq's gfx950 kernel (idolq_q8_0_gemm, DEQUANT mode); there is no other path.
+numerics: weights dequantized to the activation dtype (the fp32 value, rounded), fp32 accumulation, the product
+rounded to the output dtype before the bias is added (tools/idol_triton.py:84-89). Per kind:
+  Q8_0 (8)   libidolq's Q8_0 GEMM (idolq_q8_0_gemm, DEQUANT mode) on the GGUF blocks as they are;
+  Q4_0 (4)   the blocks re-encoded exactly as Q8_0 blocks (idolq_q4_0_to_q8_0: same scale, codes q - 8) into a
+             per-call scratch, then the same Q8_0 GEMM: the weights it multiplies are the reference's T(d * (q - 8));
+  Q4_K (44)  the matrix expanded to the activation dtype by libidolq (idolq_blocks_dequant, the reference's values)
+             into a per-call scratch, then a library GEMM (hipBLASLt through torch) with fp32 accumulation, rounded,
+             and the bias added in fp32 afterwards -- the reference's own route for its large products
+             (tools/idol_triton.py:112-117).
 """
 import torch
 
@@ -13,7 +19,7 @@ KIND_Q4_0, KIND_Q8_0, KIND_Q4_K = 4, 8, 44
 
 
 def fused_linear(value, packed, shape, kind, bias=None):
-    """Multiply FP16/BF16 activations by Q8_0 weights on the GPU (tools/idol_triton.py:94-126)."""
+    """Multiply FP16/BF16 activations by Q4_0, Q8_0 or Q4_K weights on the GPU (tools/idol_triton.py:94-126)."""
     if (not value.is_cuda or not packed.is_cuda or packed.dtype != torch.uint8
             or value.device != packed.device or value.dtype not in (torch.float16, torch.bfloat16)
             or len(shape) != 2 or value.shape[-1] != shape[1] or kind not in (KIND_Q4_0, KIND_Q8_0, KIND_Q4_K)):
@@ -26,13 +32,22 @@ def fused_linear(value, packed, shape, kind, bias=None):
         raise ValueError('invalid packed linear dimensions')
     if bias is not None and (bias.shape != (n,) or bias.device != value.device or bias.dtype != value.dtype):
         raise ValueError('invalid fused linear bias')
-    if kind != KIND_Q8_0:
-        raise NotImplementedError('only Q8_0 weights have a fused MI355X kernel')
     x = value.reshape(-1, k)
     if x.shape[0] and x.stride(-1) != 1:
         x = x.contiguous()
     m = x.shape[0]
     if not m:
         return torch.empty((*value.shape[:-1], n), device=value.device, dtype=value.dtype)
-    out = L.gemm(x, packed.reshape(-1), n, bias=bias, mode=L.MODE_DEQUANT, flags=L.FLAG_ROUND_BEFORE_BIAS)
+    w = packed.reshape(-1)
+    if kind == KIND_Q4_K:
+        dense = L.blocks_dequant(w, L.KIND_Q4_K, n, k, value.dtype)
+        out = torch.nn.functional.linear(x, dense)
+        if bias is not None:
+            out = (out.float() + bias.float()).to(value.dtype)
+        return out.reshape(*value.shape[:-1], n)
+    if kind == KIND_Q4_0:
+        w = L.q4_0_to_q8_0(w, n, k)
+    # the bias enters the epilogue as fp32, as the reference loads it (an exact widening)
+    b32 = bias.float() if bias is not None else None
+    out = L.gemm(x, w, n, bias=b32, mode=L.MODE_DEQUANT, flags=L.FLAG_ROUND_BEFORE_BIAS)
     return out.reshape(*value.shape[:-1], n)

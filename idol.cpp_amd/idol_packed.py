@@ -2,12 +2,10 @@
 tools/idol_packed.py (PackedLinear, enable_fused_packed, replace_quantized_linear_layers).
 
 Signatures, attributes (`shape`, `kind`, `packed` buffer, `bias`, `fused`), validation and error messages follow the
-reference. Differences:
-  * the fused GPU path is libidolq's gfx950 kernel (idol_hip.fused_linear) and exists for Q8_0; enable_fused_packed
-    therefore enables Q8_0 layers only;
-  * dequantize() expands Q8_0 on the GPU with libidolq's kernel (tools/idol_triton.py:_unpack_q8 semantics) and
-    F16 / Q4_0 with tensor arithmetic; the K-quant kinds are accepted as packed storage but cannot be expanded
-    (NotImplementedError).
+reference. The fused GPU path is libidolq (idol_hip.fused_linear) for Q4_0, Q8_0 and Q4_K, the kinds the reference
+fuses. dequantize() expands every kind: on the GPU with libidolq's kernels (idolq_q8_0_dequant,
+idolq_blocks_dequant), for a module kept on the host with tensor arithmetic; both compute each value with the
+reference expansion's fp32 operations (tools/idol_packed.py:25-71), then round once.
 """
 import numpy as np
 import torch
@@ -19,7 +17,7 @@ from idol_hip import fused_linear
 
 _PACKED_KINDS = (GGMLQuantizationType.F16, GGMLQuantizationType.Q8_0, GGMLQuantizationType.Q4_0,
                  GGMLQuantizationType.Q2_K, GGMLQuantizationType.Q4_K, GGMLQuantizationType.Q6_K)
-_FUSED_KINDS = {GGMLQuantizationType.Q8_0: 8}
+_FUSED_KINDS = {GGMLQuantizationType.Q4_0: 4, GGMLQuantizationType.Q8_0: 8, GGMLQuantizationType.Q4_K: 44}
 
 
 class PackedLinear(torch.nn.Module):
@@ -38,28 +36,20 @@ class PackedLinear(torch.nn.Module):
     def dequantize(self, dtype):
         """The dense (n, k) weight in `dtype` (tools/idol_packed.py:25-71)."""
         kind = self.kind
+        n, k = self.shape
         if kind == GGMLQuantizationType.F16:
             return self.packed.view(torch.float16).reshape(self.shape).to(dtype)
-        if kind == GGMLQuantizationType.Q8_0:
-            n, k = self.shape
-            if self.packed.is_cuda:
-                if dtype in L.DTYPE_CODE:
-                    return L.dequant(self.packed, n, k, dtype)
-                return L.dequant(self.packed, n, k, torch.float32).to(dtype)
-            blocks = self.packed.reshape(-1, 34)
-            scale = blocks[:, :2].contiguous().view(torch.float16).float()
-            codes = blocks[:, 2:].contiguous().view(torch.int8).float()
-            return (codes * scale).reshape(self.shape).to(dtype)
-        if kind == GGMLQuantizationType.Q4_0:
-            blocks = self.packed.reshape(-1, 18)
-            scale = blocks[:, :2].contiguous().view(torch.float16).float()
-            nib = blocks[:, 2:]
-            codes = torch.cat((nib & 15, nib >> 4), dim=1).to(torch.int16).sub_(8).float()
-            return (codes * scale).reshape(self.shape).to(dtype)
-        raise NotImplementedError(f"dequantize is not implemented for {GGMLQuantizationType(kind).name}")
+        if self.packed.is_cuda:
+            out_dtype = dtype if dtype in L.DTYPE_CODE else torch.float32
+            if kind == GGMLQuantizationType.Q8_0:
+                dense = L.dequant(self.packed, n, k, out_dtype)
+            else:
+                dense = L.blocks_dequant(self.packed, int(kind), n, k, out_dtype)
+            return dense if out_dtype == dtype else dense.to(dtype)
+        return _host_values(self.packed, kind, n, k).to(dtype)
 
     def forward(self, value):
-        """Fused kernel for Q8_0 on the GPU with 16-bit activations and no autograd; otherwise a dense product
+        """Fused kernel for Q4_0, Q8_0 and Q4_K on the GPU with 16-bit activations and no autograd; otherwise a dense product
         (tools/idol_packed.py:73-82)."""
         needs_grad = torch.is_grad_enabled() and (value.requires_grad or
                                                   (self.bias is not None and self.bias.requires_grad))
@@ -67,6 +57,51 @@ class PackedLinear(torch.nn.Module):
                 and self.kind in _FUSED_KINDS and not needs_grad):
             return fused_linear(value, self.packed, self.shape, _FUSED_KINDS[self.kind], self.bias)
         return F.linear(value, self.dequantize(value.dtype), self.bias)
+
+
+def _host_values(packed, kind, n, k):
+    """fp32 values of a packed matrix held on the host: per block format, the products and differences of the
+    reference's expansion, in fp32, without fused multiply-adds."""
+    f16 = lambda b: b.contiguous().view(torch.float16).float()  # noqa: E731
+    u = packed.reshape(-1)
+    if kind == GGMLQuantizationType.Q8_0:
+        blocks = u.reshape(-1, 34)
+        return (blocks[:, 2:].contiguous().view(torch.int8).float() * f16(blocks[:, :2])).reshape(n, k)
+    if kind == GGMLQuantizationType.Q4_0:
+        blocks = u.reshape(-1, 18)
+        nib = blocks[:, 2:]
+        q = torch.cat((nib & 15, nib >> 4), dim=1).to(torch.int16).sub_(8).float()
+        return (q * f16(blocks[:, :2])).reshape(n, k)
+    if kind == GGMLQuantizationType.Q2_K:
+        blocks = u.reshape(-1, 84)
+        pairs = blocks[:, :16]
+        sd = f16(blocks[:, 80:82]) * (pairs & 15).float()          # [blocks, 16]
+        sm = f16(blocks[:, 82:84]) * (pairs >> 4).float()
+        qs = blocks[:, 16:80].reshape(-1, 2, 1, 32)                  # [blocks, half, 1, l]
+        shift = torch.arange(0, 8, 2, dtype=torch.uint8).reshape(1, 1, 4, 1)
+        q = ((qs >> shift) & 3).reshape(-1, 16, 16).float()          # element 128 h + 32 s + l
+        return (sd.unsqueeze(2) * q - sm.unsqueeze(2)).reshape(n, k)
+    if kind == GGMLQuantizationType.Q4_K:
+        blocks = u.reshape(-1, 144)
+        s = blocks[:, 4:16].to(torch.int32)
+        a, b, c = s[:, 0:4], s[:, 4:8], s[:, 8:12]
+        sc = torch.cat((a & 63, (c & 15) | ((a >> 6) << 4)), dim=1).float()
+        mn = torch.cat((b & 63, (c >> 4) | ((b >> 6) << 4)), dim=1).float()
+        sd = f16(blocks[:, 0:2]) * sc
+        sm = f16(blocks[:, 2:4]) * mn
+        qs = blocks[:, 16:].reshape(-1, 4, 1, 32)
+        q = ((qs >> torch.tensor([0, 4], dtype=torch.uint8).reshape(1, 1, 2, 1)) & 15).reshape(-1, 8, 32).float()
+        return (sd.unsqueeze(2) * q - sm.unsqueeze(2)).reshape(n, k)
+    if kind == GGMLQuantizationType.Q6_K:
+        blocks = u.reshape(-1, 210)
+        ql = blocks[:, :128].reshape(-1, 2, 1, 64)
+        qh = blocks[:, 128:192].reshape(-1, 2, 1, 32)
+        lo = ((ql >> torch.tensor([0, 4], dtype=torch.uint8).reshape(1, 1, 2, 1)) & 15).reshape(-1, 2, 4, 32)
+        hi = ((qh >> torch.arange(0, 8, 2, dtype=torch.uint8).reshape(1, 1, 4, 1)) & 3).reshape(-1, 2, 4, 32)
+        q = (lo.to(torch.int16) | (hi.to(torch.int16) << 4)).sub_(32).reshape(-1, 16, 16).float()
+        sd = f16(blocks[:, 208:210]) * blocks[:, 192:208].contiguous().view(torch.int8).float()
+        return (sd.unsqueeze(2) * q).reshape(n, k)
+    raise NotImplementedError(f"dequantize is not implemented for {GGMLQuantizationType(kind).name}")
 
 
 def enable_fused_packed(model):

@@ -15,6 +15,7 @@ ACT_NONE, ACT_GELU_ERF, ACT_GELU_TANH, ACT_RELU, ACT_SILU = 0, 1, 2, 3, 4
 MODE_AUTO, MODE_DEQUANT, MODE_EXACT, MODE_INT8 = 0, 1, 2, 3
 FLAG_ROUND_BEFORE_BIAS, FLAG_TILED_WEIGHTS = 1, 2
 EINVAL, ELAUNCH, ENOSUPPORT = -1, -2, -3
+KIND_F16, KIND_Q4_0, KIND_Q8_0, KIND_Q2_K, KIND_Q4_K, KIND_Q6_K = 1, 2, 8, 10, 12, 14
 
 DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 Q8_0_BLOCK, Q8_0_BYTES = 32, 34
@@ -47,6 +48,9 @@ _SIGNATURES = {
     "idolq_rms_heads": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _vp, _vp]),
     "idolq_add_gated": (_int, [_vp, _int, _i64, _vp, _int, _i64, _i64, _i64, _vp, _vp]),
     "idolq_level_embed": (_int, [ctypes.c_float, _vp, _i64, _vp, _vp]),
+    "idolq_blocks_bytes": (_i64, [_int, _i64, _i64]),
+    "idolq_blocks_dequant": (_int, [_vp, _int, _i64, _i64, _vp, _int, _vp]),
+    "idolq_q4_0_to_q8_0": (_int, [_vp, _i64, _i64, _vp, _vp]),
 }
 
 _lib = None
@@ -373,4 +377,32 @@ def level_embed(resolution, freqs, out=None):
     if out is None:
         out = torch.empty(2 * half, device=freqs.device, dtype=torch.float32)
     _check(lib.idolq_level_embed(float(resolution), _ptr(freqs), half, _ptr(out), _stream(freqs.device)))
+    return out
+
+
+def blocks_bytes(kind, n, k):
+    return int(load().idolq_blocks_bytes(kind, n, k))
+
+
+def blocks_dequant(w, kind, n, k, dtype, out=None):
+    """The dense [n, k] matrix in `dtype` of GGUF blocks of format `kind` (KIND_*) on the GPU."""
+    lib = load()
+    _require_cuda(w, out)
+    if w.dtype != torch.uint8 or not w.is_contiguous() or w.numel() != blocks_bytes(kind, n, k) or w.numel() == 0:
+        raise ValueError("packed weight size does not match its shape and format")
+    if out is None:
+        out = torch.empty((n, k), device=w.device, dtype=dtype)
+    _check(lib.idolq_blocks_dequant(_ptr(w), kind, n, k, _ptr(out), _code(out), _stream(w.device)))
+    return out
+
+
+def q4_0_to_q8_0(w, n, k, out=None):
+    """Q8_0 blocks holding exactly the values of Q4_0 blocks [n, k]."""
+    lib = load()
+    _require_cuda(w, out)
+    if w.dtype != torch.uint8 or not w.is_contiguous() or w.numel() != blocks_bytes(KIND_Q4_0, n, k):
+        raise ValueError("Q4_0 weight size does not match its shape")
+    if out is None:
+        out = torch.empty(q8_0_bytes(n, k), device=w.device, dtype=torch.uint8)
+    _check(lib.idolq_q4_0_to_q8_0(_ptr(w), n, k, _ptr(out), _stream(w.device)))
     return out

@@ -28,6 +28,16 @@ enum { IDOLQ_F32 = 0, IDOLQ_F16 = 1, IDOLQ_BF16 = 2 };
  * activation (src/decoders.cpp:88). */
 enum { IDOLQ_ACT_NONE = 0, IDOLQ_ACT_GELU_ERF = 1, IDOLQ_ACT_GELU_TANH = 2, IDOLQ_ACT_RELU = 3, IDOLQ_ACT_SILU = 4 };
 
+/* GGUF block formats (the ggml type codes) of the packed-linear surface. */
+enum {
+    IDOLQ_KIND_F16 = 1,
+    IDOLQ_KIND_Q4_0 = 2,
+    IDOLQ_KIND_Q8_0 = 8,
+    IDOLQ_KIND_Q2_K = 10,
+    IDOLQ_KIND_Q4_K = 12,
+    IDOLQ_KIND_Q6_K = 14
+};
+
 /* GEMM arithmetic.
  *   DEQUANT  weights dequantized to the activation's 16-bit type (bf16 or fp16 of fp32(d) * q) in LDS, MFMA with fp32
  *            accumulation over the whole depth: the numerics of the reference's fused GPU path.
@@ -157,6 +167,20 @@ int idolq_linear_f32(const void* x, int x_dtype, int64_t m, int64_t k, int64_t l
 /* Copies a [rows x cols] block between dtypes and strides (a column slice of a wider row is a pointer offset). */
 int idolq_copy2d(const void* src, int src_dtype, int64_t lds, void* dst, int dst_dtype, int64_t ldd, int64_t rows,
                  int64_t cols, void* stream);
+
+/* ---- Other block formats (tools/idol_packed.py:25-71, tools/idol_triton.py:48-82). ---- */
+
+/* Bytes of an [n x k] matrix in block format `kind` (0 when k is not a multiple of the block's value count). */
+int64_t idolq_blocks_bytes(int kind, int64_t n, int64_t k);
+
+/* out[r, c] = out_dtype(w[r, c]) for the whole [n x k] matrix in block format `kind` (Q4_0, Q8_0, Q2_K, Q4_K, Q6_K,
+ * F16), out row stride k, 16-byte aligned. Each value is computed in fp32 with the reference expansion's operations
+ * (PackedLinear.dequantize, tools/idol_packed.py:25-71), then rounded once. */
+int idolq_blocks_dequant(const uint8_t* w, int kind, int64_t n, int64_t k, void* out, int out_dtype, void* stream);
+
+/* Re-encodes Q4_0 blocks [n x k] as Q8_0 blocks (same fp16 scale, codes q - 8): exact, so every Q8_0 GEMM mode
+ * computes the Q4_0 layer's products (the Q4_0 case of tools/idol_triton.py:48-60). */
+int idolq_q4_0_to_q8_0(const uint8_t* w, int64_t n, int64_t k, uint8_t* out, void* stream);
 
 /* ---- The real decoders' operators (src/decoders.cpp), fp32 surface, in the reference's operation order. ---- */
 

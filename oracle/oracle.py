@@ -437,3 +437,100 @@ class RefDecoders:
         if ref_lib().ref_decoders_gaussian_features(self._h, points, points.shape[0], cond, cond.shape[0], out):
             raise RuntimeError(ref_lib().ref_last_error().decode())
         return out
+
+
+# ------------------------------------------------------------------------------------------------ other block formats
+# GGUF block formats restated element by element from the ggml layouts (ggml-quants.c dequantize_row_*), the layouts
+# the reference's expansion (tools/idol_packed.py:25-71) and fused kernel (tools/idol_triton.py:48-82) decode: for
+# every element e of a block, the byte and bit position of its code and the index of its scale group. Values are
+# products and differences in fp32 without fused multiply-adds.
+KIND_F16, KIND_Q4_0, KIND_Q8_0, KIND_Q2_K, KIND_Q4_K, KIND_Q6_K = 1, 2, 8, 10, 12, 14
+BLOCK_SHAPE = {KIND_Q4_0: (32, 18), KIND_Q8_0: (32, 34), KIND_Q2_K: (256, 84), KIND_Q4_K: (256, 144),
+               KIND_Q6_K: (256, 210)}
+
+
+def _f16(blocks, off):
+    return np.ascontiguousarray(blocks[:, off:off + 2]).view("<f2").astype(np.float32)[:, 0]
+
+
+def blocks_values(raw, kind, n, k):
+    """fp32 [n, k] values of GGUF blocks of format `kind` (a uint8 array of n * k / values * bytes)."""
+    values, size = BLOCK_SHAPE[kind]
+    blocks = np.asarray(raw, np.uint8).reshape(-1, size)
+    nb = blocks.shape[0]
+    out = np.empty((nb, values), np.float32)
+    e = np.arange(values)
+    if kind == KIND_Q8_0:
+        d = _f16(blocks, 0)
+        q = blocks[:, 2:].view(np.int8).astype(np.float32)
+        out[:] = d[:, None] * q
+    elif kind == KIND_Q4_0:
+        d = _f16(blocks, 0)
+        byte = blocks[:, 2 + (e % 16)]
+        q = np.where(e < 16, byte & 15, byte >> 4).astype(np.int32) - 8
+        out[:] = d[:, None] * q.astype(np.float32)
+    elif kind == KIND_Q2_K:
+        d, dmin = _f16(blocks, 80), _f16(blocks, 82)
+        h, s, l = e // 128, (e % 128) // 32, e % 32
+        q = (blocks[:, 16 + 32 * h + l] >> (2 * s)) & 3
+        pair = blocks[:, e // 16]
+        sd = d[:, None] * (pair & 15).astype(np.float32)
+        sm = dmin[:, None] * (pair >> 4).astype(np.float32)
+        out[:] = sd * q.astype(np.float32) - sm
+    elif kind == KIND_Q4_K:
+        d, dmin = _f16(blocks, 0), _f16(blocks, 2)
+        j = e // 32
+        sc = np.empty((nb, 8), np.int32)
+        mn = np.empty((nb, 8), np.int32)
+        s = blocks[:, 4:16].astype(np.int32)
+        for g in range(8):
+            if g < 4:
+                sc[:, g] = s[:, g] & 63
+                mn[:, g] = s[:, g + 4] & 63
+            else:
+                sc[:, g] = (s[:, g + 4] & 15) | ((s[:, g - 4] >> 6) << 4)
+                mn[:, g] = (s[:, g + 4] >> 4) | ((s[:, g] >> 6) << 4)
+        byte = blocks[:, 16 + 32 * (j // 2) + e % 32]
+        q = np.where(j % 2 == 0, byte & 15, byte >> 4).astype(np.float32)
+        sd = d[:, None] * sc[:, j].astype(np.float32)
+        sm = dmin[:, None] * mn[:, j].astype(np.float32)
+        out[:] = sd * q - sm
+    elif kind == KIND_Q6_K:
+        d = _f16(blocks, 208)
+        h, t, l = e // 128, (e % 128) // 32, e % 32
+        lo_byte = blocks[:, 64 * h + 32 * (t % 2) + l]
+        lo = np.where(t >= 2, lo_byte >> 4, lo_byte & 15).astype(np.int32)
+        hi = ((blocks[:, 128 + 32 * h + l] >> (2 * t)) & 3).astype(np.int32)
+        sc = blocks[:, 192:208].view(np.int8).astype(np.float32)
+        sd = d[:, None] * sc[:, e // 16]
+        out[:] = sd * ((lo | (hi << 4)) - 32).astype(np.float32)
+    else:
+        raise ValueError("unsupported block format")
+    return out.reshape(n, k)
+
+
+def q4_0_to_q8_0(raw, n, k):
+    """Q8_0 blocks with the values of Q4_0 blocks: the same fp16 scale, codes q - 8."""
+    b4 = np.asarray(raw, np.uint8).reshape(-1, 18)
+    out = np.empty((b4.shape[0], 34), np.uint8)
+    out[:, :2] = b4[:, :2]
+    q = np.concatenate([b4[:, 2:] & 15, b4[:, 2:] >> 4], axis=1).astype(np.int16) - 8
+    out[:, 2:] = q.astype(np.int8).view(np.uint8)
+    return out.reshape(-1)
+
+
+def q4_0_quantize(w):
+    """Q4_0 blocks of fp32 w [n, k] by ggml's rule: per 32 values, m = the value of largest magnitude, d = m / -8,
+    q = min(15, trunc(x / d + 8.5)) (quantize_row_q4_0_ref), d stored as fp16."""
+    w = np.asarray(w, np.float32)
+    n, k = w.shape
+    g = w.reshape(-1, 32)
+    idx = np.argmax(np.abs(g), axis=1)
+    m = g[np.arange(g.shape[0]), idx]
+    d = (m / np.float32(-8.0)).astype(np.float32)
+    inv = np.where(d != 0, np.float32(1.0) / np.where(d != 0, d, np.float32(1.0)), np.float32(0.0)).astype(np.float32)
+    q = np.minimum(15, np.trunc(g * inv[:, None] + np.float32(8.5)).astype(np.int32)).astype(np.uint8)
+    out = np.empty((g.shape[0], 18), np.uint8)
+    out[:, :2] = d.astype(np.float16).reshape(-1, 1).view(np.uint8)
+    out[:, 2:] = q[:, :16] | (q[:, 16:] << 4)
+    return out.reshape(-1)
