@@ -23,8 +23,24 @@ class GGMLQuantizationType(enum.IntEnum):
     Q5_K = 13
     Q6_K = 14
     Q8_K = 15
+    I8 = 24
+    I16 = 25
+    I32 = 26
+    I64 = 27
+    F64 = 28
     BF16 = 30
 
+
+# (values, bytes) per block of every type a GGUF container may hold that this package reads (ggml's type traits).
+TYPE_SIZE = {
+    GGMLQuantizationType.F32: (1, 4), GGMLQuantizationType.F16: (1, 2), GGMLQuantizationType.BF16: (1, 2),
+    GGMLQuantizationType.F64: (1, 8), GGMLQuantizationType.I8: (1, 1), GGMLQuantizationType.I16: (1, 2),
+    GGMLQuantizationType.I32: (1, 4), GGMLQuantizationType.I64: (1, 8),
+    GGMLQuantizationType.Q4_0: (32, 18), GGMLQuantizationType.Q4_1: (32, 20), GGMLQuantizationType.Q5_0: (32, 22),
+    GGMLQuantizationType.Q5_1: (32, 24), GGMLQuantizationType.Q8_0: (32, 34), GGMLQuantizationType.Q8_1: (32, 36),
+    GGMLQuantizationType.Q2_K: (256, 84), GGMLQuantizationType.Q3_K: (256, 110), GGMLQuantizationType.Q4_K: (256, 144),
+    GGMLQuantizationType.Q5_K: (256, 176), GGMLQuantizationType.Q6_K: (256, 210), GGMLQuantizationType.Q8_K: (256, 292),
+}
 
 # (block size in values, block size in bytes) of the block formats the packed layers accept.
 BLOCK_LAYOUT = {

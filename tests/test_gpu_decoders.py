@@ -205,3 +205,35 @@ def test_model_width_export_matches_the_reference_decoders(tmp_path):
     r_oct, r_gs = norm_rel(oct_, want_oct), norm_rel(gs, want_gs)
     print(f"dim 1024: octree {r_oct:.3e} gaussian {r_gs:.3e}")
     assert r_oct < 2e-5 and r_gs < 2e-5
+
+
+@pytest.mark.parametrize("quant", ["Q8_0", "Q4_0"])
+def test_decoders_from_gguf_match_the_reference(tmp_path, quant):
+    # an Idol GGUF (Q8_0 or Q4_0 matrices, F32 / F16 vectors) run three ways: the reference's decoders on the
+    # materialized native export, this build on the same export, and this build straight from the GGUF
+    import idol_gguf as G
+    from ggml_types import GGMLQuantizationType as Q
+    from gguf_fixture import write_idol_gguf
+    write_idol_gguf(tmp_path / "d.gguf", quant=getattr(Q, quant))
+    m = G.IdolGGUF(tmp_path / "d.gguf")
+    G.materialize(m, tmp_path / "native")
+    rng = np.random.default_rng(31)
+    anchors = rng.uniform(0, 1, (45, 3)).astype(np.float32)
+    cond = rng.standard_normal((23, 16)).astype(np.float32)
+    K.set_quant_kernel(0)
+    try:
+        a = _run(Decoders(tmp_path / "native"), anchors, cond, 16.0)
+        b = _run(Decoders(G.decoder_export(m)), anchors, cond, 16.0)
+    finally:
+        K.set_quant_kernel(-1)
+    assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+    if O.ref_available():
+        ref = O.RefDecoders(tmp_path / "native")
+        O.ref_lib().ref_set_quant_kernel(0)
+        try:
+            r_oct, r_gs = ref.octree_logits(anchors, 16.0, cond), ref.gaussian_features(anchors, cond)
+        finally:
+            O.ref_lib().ref_set_quant_kernel(-1)
+            ref.close()
+        print(f"{quant}: octree {norm_rel(a[0], r_oct):.3e} gaussian {norm_rel(a[1], r_gs):.3e}")
+        assert norm_rel(a[0], r_oct) < 2e-5 and norm_rel(a[1], r_gs) < 2e-5
