@@ -17,7 +17,8 @@ Also reported, in the same JSON line:
   fused_*        fused_linear per fused kind (Q8_0, Q4_0, Q4_K) at the up-projection shape, with bias
   decoders_*     the real model's octree and Gaussian decoders (dim 1024, 16 heads, 4 and 16 blocks, 32 Gaussians per
                  anchor) on 1024 anchors and 8192 latent tokens, fp32 activations, the reference's float-kernel
-                 numerics, unless --no-decoders; with the reference's own decoders timed on the host beside them
+                 numerics, unless --no-decoders; with the reference's own decoders timed on the host beside them;
+  decode_ms      Decoders.decode end to end: 262144 Gaussians (8192 anchors), octree descent to level 8
   cpu_baseline   the reference's own CPU kernels (oracle/_ref, float kernel, all host cores) on the same MLP block
 """
 import argparse
@@ -246,7 +247,7 @@ def run_decoder_mlp(args):
     return out, model
 
 
-DEC_ROWS, DEC_TOKENS, DEC_LEVEL = 1024, 8192, 8
+DEC_ROWS, DEC_TOKENS, DEC_LEVEL, DEC_GAUSSIANS = 1024, 8192, 8, 262144
 
 
 def _decoder_config(oct_blocks=4, gs_blocks=16):
@@ -296,8 +297,25 @@ def run_decoders(args):
             out[name] = sorted(times)[2] * 1e3
     finally:
         K.set_quant_kernel(-1)
+    # decode end to end (octree descent to level 8 with systematic resampling, the Gaussian decoder on the anchors,
+    # activation): 262144 Gaussians = 8192 anchors of 32
+    cond_np = cond.cpu().numpy()
+    K.set_quant_kernel(0)
+    try:
+        dec.decode(cond_np, DEC_TOKENS, DEC_GAUSSIANS, DEC_LEVEL, 7)
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            cloud = dec.decode(cond_np, DEC_TOKENS, DEC_GAUSSIANS, DEC_LEVEL, 7)
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t0)
+    finally:
+        K.set_quant_kernel(-1)
+    out["decode"] = sorted(times)[1] * 1e3
     f_oct, f_gs = decoder_flop(cfg, DEC_ROWS, DEC_TOKENS)
     return {"decoders_oct_ms": round(out["oct"], 3), "decoders_gs_ms": round(out["gs"], 3),
+            "decode_ms": round(out["decode"], 1), "decode_gaussians": cloud.size(),
             "decoders_tflops": round((f_oct + f_gs) / ((out["oct"] + out["gs"]) * 1e-3) / 1e12, 2),
             "decoders_config": f"dim 1024, 16 heads, 4 octree + 16 Gaussian blocks, 32 per anchor; {DEC_ROWS} anchors, "
                                f"{DEC_TOKENS} latent tokens, fp32, float-kernel numerics"}

@@ -143,6 +143,44 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
     }
 }
 
+// Raw Gaussian features -> activated Gaussians, one thread per (anchor, Gaussian) (src/decoders.cpp:393-431
+// to_gaussians). rep: perturbe, kernel, lr_xyz, lr_dc, lr_opacity, lr_scaling, lr_rotation, scale_offset (inverse
+// softplus of the scaling bias), opacity_offset (inverse sigmoid of the opacity bias), base_offset_scale.
+__device__ __forceinline__ float softplus(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+
+__global__ __launch_bounds__(256) void to_gaussians_kernel(const float* __restrict__ anchors, int64_t rows,
+                                                           const float* __restrict__ features, int G,
+                                                           const float* __restrict__ pert, const float* __restrict__ rep,
+                                                           float* __restrict__ xyz, float* __restrict__ f_dc,
+                                                           float* __restrict__ scale, float* __restrict__ rotation,
+                                                           float* __restrict__ opacity) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * G) return;
+    const int64_t a = i / G;
+    const int g = (int)(i - a * G);
+    const float perturbe = rep[0], kernel = rep[1], lr_xyz = rep[2], lr_dc = rep[3], lr_opacity = rep[4],
+                lr_scaling = rep[5], lr_rotation = rep[6], scale_offset = rep[7], opacity_offset = rep[8],
+                base_offset_scale = rep[9];
+    const float* f = features + a * (int64_t)G * 15;
+    const int xyz0 = 0, dc0 = G * 3, sc0 = G * 6, rot0 = G * 9, op0 = G * 13, os0 = G * 14;
+    const float offset_scale = softplus(f[os0 + g] + base_offset_scale);
+    for (int c = 0; c < 3; ++c) {
+        const float o = tanhf(f[xyz0 + g * 3 + c] * lr_xyz + pert[g * 3 + c]) * 0.5f * perturbe * offset_scale;
+        xyz[i * 3 + c] = (o + anchors[a * 3 + c]) - 0.5f;
+        f_dc[i * 3 + c] = f[dc0 + g * 3 + c] * lr_dc;
+        const float sv = softplus(f[sc0 + g * 3 + c] * lr_scaling + scale_offset);
+        scale[i * 3 + c] = sqrtf(sv * sv + kernel * kernel);
+    }
+    float q[4], norm = 0.0f;
+    for (int c = 0; c < 4; ++c) {
+        q[c] = f[rot0 + g * 4 + c] * lr_rotation + (c == 0 ? 1.0f : 0.0f);
+        norm += q[c] * q[c];
+    }
+    norm = fmaxf(sqrtf(norm), 1e-12f);
+    for (int c = 0; c < 4; ++c) rotation[i * 4 + c] = q[c] / norm;
+    opacity[i] = 1.0f / (1.0f + expf(-(f[op0 + g] * lr_opacity + opacity_offset)));
+}
+
 unsigned grid_of(int64_t items) {
     const int64_t g = (items + 255) / 256;
     return (unsigned)(g < 1 ? 1 : g > 1048576 ? 1048576 : g);
@@ -211,4 +249,17 @@ extern "C" int idolq_gemm_f32(const float* x, int64_t m, int64_t k, int64_t ldx,
     hipLaunchKernelGGL(gemm_f32_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), x, (int)m, (int)k, ldx,
                        w, (int)n, bias, residual, ldr, act, y, ldy);
     return check_launch("gemm_f32_kernel");
+}
+
+extern "C" int idolq_to_gaussians(const float* anchors, int64_t rows, const float* features, int64_t per_anchor,
+                                  const float* perturbation, const float* rep, float* xyz, float* f_dc, float* scale,
+                                  float* rotation, float* opacity, void* stream) {
+    if (rows < 0 || per_anchor <= 0 || per_anchor > 4096) return fail(IDOLQ_EINVAL, "to_gaussians: bad rows or per_anchor");
+    if (rows == 0) return IDOLQ_OK;
+    if (!anchors || !features || !perturbation || !rep || !xyz || !f_dc || !scale || !rotation || !opacity)
+        return fail(IDOLQ_EINVAL, "to_gaussians: null pointer");
+    hipLaunchKernelGGL(to_gaussians_kernel, dim3((unsigned)((rows * per_anchor + 255) / 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), anchors, rows, features, (int)per_anchor, perturbation, rep,
+                       xyz, f_dc, scale, rotation, opacity);
+    return check_launch("to_gaussians_kernel");
 }

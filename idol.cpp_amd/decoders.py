@@ -306,3 +306,200 @@ def synthetic_export(cfg, seed=0, device="cuda"):
     vec("gs.pos_embedder.freqs", freqs)
     vec("oct.l_embedder.freqs", torch.exp(-np.log(1024) * torch.arange(0, 128, dtype=torch.float32) / 128).numpy())
     return ex
+
+
+# ------------------------------------------------------------------------------------------------ sampling
+class MT19937_64:
+    """std::mt19937_64 (the 64-bit Mersenne Twister of Matsumoto and Nishimura, as the C++ standard specifies it:
+    n = 312, m = 156, r = 31, a = 0xB5026F5AA96619E9, tempering (29, 0x5555555555555555), (17, 0x71D67FFFEDA60000),
+    (37, 0xFFF7EEE000000000), 43; seeding multiplier 6364136223846793005), generated 312 outputs at a time with
+    numpy, and std::uniform_real_distribution<float>(0, 1) on top as libstdc++ computes it (generate_canonical: one
+    64-bit draw, float(x) / 2^64, 1 mapped to the float below 1)."""
+    _N, _M = 312, 156
+    _A = np.uint64(0xB5026F5AA96619E9)
+    _UPPER, _LOWER = np.uint64(0xFFFFFFFF80000000), np.uint64(0x7FFFFFFF)
+
+    def __init__(self, seed):
+        mt = np.empty(self._N, np.uint64)
+        mt[0] = np.uint64(seed & 0xFFFFFFFFFFFFFFFF)
+        with np.errstate(over="ignore"):
+            for i in range(1, self._N):
+                prev = int(mt[i - 1])
+                mt[i] = np.uint64((6364136223846793005 * (prev ^ (prev >> 62)) + i) & 0xFFFFFFFFFFFFFFFF)
+        self.mt = mt
+        self.buf = np.empty(0, np.uint64)
+        self.pos = 0
+
+    def _twist(self):
+        mt, N, M = self.mt, self._N, self._M
+        one = np.uint64(1)
+
+        def mix(cur, nxt, far):
+            x = (cur & self._UPPER) | (nxt & self._LOWER)
+            return far ^ (x >> one) ^ np.where((x & one) != 0, self._A, np.uint64(0))
+
+        mt[:N - M] = mix(mt[:N - M], mt[1:N - M + 1], mt[M:])            # far values not yet replaced
+        mt[N - M:N - 1] = mix(mt[N - M:N - 1], mt[N - M + 1:], mt[:M - 1])  # far values of this round
+        mt[N - 1] = mix(mt[N - 1:], mt[:1], mt[M - 1:M])[0]
+        y = mt.copy()
+        y ^= (y >> np.uint64(29)) & np.uint64(0x5555555555555555)
+        y ^= (y << np.uint64(17)) & np.uint64(0x71D67FFFEDA60000)
+        y ^= (y << np.uint64(37)) & np.uint64(0xFFF7EEE000000000)
+        y ^= y >> np.uint64(43)
+        self.buf, self.pos = y, 0
+
+    def raw(self, count):
+        """The next `count` 64-bit outputs."""
+        out = np.empty(count, np.uint64)
+        filled = 0
+        while filled < count:
+            if self.pos == self.buf.size:
+                self._twist()
+            take = min(count - filled, self.buf.size - self.pos)
+            out[filled:filled + take] = self.buf[self.pos:self.pos + take]
+            self.pos += take
+            filled += take
+        return out
+
+    def uniform(self, count):
+        """The next `count` uniform floats in [0, 1)."""
+        f = self.raw(count).astype(np.float32) * np.float32(2.0 ** -64)
+        return np.where(f >= np.float32(1.0), np.nextafter(np.float32(1.0), np.float32(0.0)), f).astype(np.float32)
+
+
+_BELOW_ONE = np.float32(1.0) - np.float32(1e-7)
+
+
+def _expf(x):
+    """float32 exp, rounded from the double result."""
+    return np.exp(x.astype(np.float64)).astype(np.float32)
+
+
+def descend_octree(logits_fn, num_points, level, seed):
+    """The octree descent of Decoders::sample_anchors (src/decoders.cpp:335-391): from the root cell, per level, the
+    children's logits of every occupied cell (logits_fn(centres [cells, 3] fp32, resolution) -> [cells, 8]), a
+    softmax, and systematic resampling of the cell's points among its children with one uniform draw per cell; then
+    each point placed uniformly inside its leaf cell. Host arithmetic in fp32 with the reference's operation order;
+    the draws come from MT19937_64(seed) in the reference's order. Returns num_points x 3 fp32."""
+    if num_points < 1 or level < 1 or level > 20:
+        raise ValueError("sample_anchors: bad num_points or level")
+    rng = MT19937_64(seed)
+    coords = np.zeros((1, 3), np.uint32)
+    counts = np.array([num_points], np.int64)
+    bits = np.array([[c & 1, (c >> 1) & 1, (c >> 2) & 1] for c in range(8)], np.uint32)
+    for lv in range(1, level + 1):
+        res_p = np.float32(1 << (lv - 1))
+        centres = ((coords.astype(np.float32) + np.float32(0.5)) / res_p).astype(np.float32)
+        logits = np.asarray(logits_fn(centres, float(1 << lv)), np.float32).reshape(-1, 8)
+        mx = logits.max(axis=1)
+        e = _expf(logits - mx[:, None])
+        total = np.zeros(len(counts), np.float32)
+        for c in range(8):
+            total = (total + e[:, c]).astype(np.float32)
+        cdf = np.empty_like(e)
+        acc = np.zeros(len(counts), np.float32)
+        for c in range(8):
+            acc = (acc + (e[:, c] / total).astype(np.float32)).astype(np.float32)
+            cdf[:, c] = np.minimum(acc, _BELOW_ONE)
+        n = counts.astype(np.float32)
+        u0 = (rng.uniform(len(counts)) / n).astype(np.float32)
+        owner = np.repeat(np.arange(len(counts)), counts)
+        k = (np.arange(owner.size) - np.repeat(np.cumsum(counts) - counts, counts)).astype(np.float32)
+        u = np.minimum((u0[owner] + (k / n[owner]).astype(np.float32)).astype(np.float32), _BELOW_ONE)
+        child = np.minimum(7, (cdf[owner] < u[:, None]).sum(axis=1))
+        got = np.zeros((len(counts), 8), np.int64)
+        np.add.at(got, (owner, child), 1)
+        parent, which = np.nonzero(got)
+        coords = coords[parent] * np.uint32(2) + bits[which]
+        counts = got[parent, which]
+    cells = np.float32(1 << level)
+    cell_of = np.repeat(np.arange(len(counts)), counts)
+    draws = rng.uniform(3 * num_points).reshape(num_points, 3)
+    return ((coords[cell_of].astype(np.float32) + draws) / cells).astype(np.float32)
+
+
+class GaussianCloud:
+    """Activated Gaussians (include/idol/decoders.hpp:22-30): xyz, f_dc, scale [n, 3], rotation [n, 4] (w first),
+    opacity [n], fp32 tensors (on the GPU as decode returns them)."""
+
+    def __init__(self, xyz, f_dc, scale, rotation, opacity):
+        self.xyz, self.f_dc, self.scale, self.rotation, self.opacity = xyz, f_dc, scale, rotation, opacity
+
+    def size(self):
+        return int(self.opacity.numel())
+
+
+def _rep_vector(dec):
+    """The to_gaussians constants: the rep fields, the inverse softplus of the scaling bias and the inverse sigmoid
+    of the opacity bias (computed in double, as the reference does), and the base offset scale."""
+    r = dec.rep
+    sb, ob = float(r.scaling_bias), float(r.opacity_bias)
+    scale_offset = np.float32(sb + np.log(-np.expm1(-sb)))
+    opacity_offset = np.float32(np.log(ob / (1.0 - ob)))
+    return torch.tensor([r.perturbe, r.kernel, r.lr_xyz, r.lr_dc, r.lr_opacity, r.lr_scaling, r.lr_rotation,
+                         scale_offset, opacity_offset, dec.base_offset_scale], dtype=torch.float32, device=dec.device)
+
+
+def _sample_anchors(self, cond, cond_rows, num_points, level, seed):
+    """Decoders::sample_anchors: the octree descent with this build's octree_logits on the GPU (num_points x 3 fp32,
+    on the host). The draws follow the reference's generator, so given the same logits the anchors are the
+    reference's; logits differing in the last bits can move a point to a sibling cell where a draw falls on a
+    cumulative-probability boundary."""
+    cond_t = self._f32(cond, "cond")[:cond_rows]
+
+    def logits(centres, resolution):
+        x = torch.from_numpy(centres).to(self.device)
+        return self.octree_logits(x, x.shape[0], resolution, cond_t, cond_rows).cpu().numpy()
+
+    return descend_octree(logits, num_points, level, seed)
+
+
+def _to_gaussians(self, anchors, rows, features):
+    """Decoders::to_gaussians on the GPU: anchors [rows, 3], features [rows, per_anchor * 15] -> GaussianCloud."""
+    a = self._f32(anchors, "anchors")[:rows]
+    f = self._f32(features, "features")[:rows]
+    out = L.to_gaussians(a, f, self.cfg.per_anchor, self.perturbation, _rep_vector(self))
+    return GaussianCloud(out["xyz"], out["f_dc"], out["scale"], out["rotation"], out["opacity"])
+
+
+def _decode(self, cond, cond_rows, num_gaussians, level, seed):
+    """Decoders::decode (src/decoders.cpp:434-442): sample_anchors, gaussian_features, to_gaussians; num_gaussians
+    rounded down to a multiple of per_anchor (at least one anchor)."""
+    G = self.cfg.per_anchor
+    anchors = max(1, num_gaussians // G)
+    points = torch.from_numpy(self.sample_anchors(cond, cond_rows, anchors, level, seed)).to(self.device)
+    cond_t = self._f32(cond, "cond")[:cond_rows]
+    features = self.gaussian_features(points, anchors, cond_t, cond_rows)
+    return self.to_gaussians(points, anchors, features)
+
+
+Decoders.sample_anchors = _sample_anchors
+Decoders.to_gaussians = _to_gaussians
+Decoders.decode = _decode
+
+
+def write_gaussian_ply(cloud, path):
+    """A binary little-endian 3DGS PLY of the cloud, turned from z-up to y-up ((x, y, z) -> (x, -z, y), the rotation
+    premultiplied by +90 degrees about x), opacity as a logit and scales as logs (src/decoders.cpp:444-476)."""
+    xyz, f_dc, scale, rot, op = (np.asarray(t.detach().cpu() if isinstance(t, torch.Tensor) else t, np.float32)
+                                 for t in (cloud.xyz, cloud.f_dc, cloud.scale, cloud.rotation, cloud.opacity))
+    n = op.size
+    names = ["x", "y", "z", "nx", "ny", "nz", "f_dc_0", "f_dc_1", "f_dc_2", "opacity", "scale_0", "scale_1",
+             "scale_2", "rot_0", "rot_1", "rot_2", "rot_3"]
+    head = "ply\nformat binary_little_endian 1.0\nelement vertex %d\n" % n
+    head += "".join(f"property float {name}\n" for name in names) + "end_header\n"
+    row = np.zeros((n, 17), np.float32)
+    xyz, rot = xyz.reshape(n, 3), rot.reshape(n, 4)
+    row[:, 0], row[:, 1], row[:, 2] = xyz[:, 0], -xyz[:, 2], xyz[:, 1]
+    row[:, 6:9] = f_dc.reshape(n, 3)
+    o = np.minimum(np.maximum(op, np.float32(1e-6)), np.float32(1.0) - np.float32(1e-6)).astype(np.float32)
+    row[:, 9] = np.log((o / (np.float32(1.0) - o)).astype(np.float64)).astype(np.float32)
+    row[:, 10:13] = np.log(np.maximum(scale.reshape(n, 3), np.float32(1e-6)).astype(np.float64)).astype(np.float32)
+    h = np.sqrt(np.float32(0.5))
+    row[:, 13] = h * rot[:, 0] - h * rot[:, 1]
+    row[:, 14] = h * rot[:, 1] + h * rot[:, 0]
+    row[:, 15] = h * rot[:, 2] - h * rot[:, 3]
+    row[:, 16] = h * rot[:, 3] + h * rot[:, 2]
+    with open(path, "wb") as f:
+        f.write(head.encode("ascii"))
+        f.write(row.astype("<f4").tobytes())

@@ -49,6 +49,7 @@ _SIGNATURES = {
     "idolq_add_gated": (_int, [_vp, _int, _i64, _vp, _int, _i64, _i64, _i64, _vp, _vp]),
     "idolq_level_embed": (_int, [ctypes.c_float, _vp, _i64, _vp, _vp]),
     "idolq_blocks_bytes": (_i64, [_int, _i64, _i64]),
+    "idolq_to_gaussians": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "idolq_blocks_dequant": (_int, [_vp, _int, _i64, _i64, _vp, _int, _vp]),
     "idolq_q4_0_to_q8_0": (_int, [_vp, _i64, _i64, _vp, _vp]),
 }
@@ -405,4 +406,25 @@ def q4_0_to_q8_0(w, n, k, out=None):
     if out is None:
         out = torch.empty(q8_0_bytes(n, k), device=w.device, dtype=torch.uint8)
     _check(lib.idolq_q4_0_to_q8_0(_ptr(w), n, k, _ptr(out), _stream(w.device)))
+    return out
+
+
+def to_gaussians(anchors, features, per_anchor, perturbation, rep):
+    """Activated Gaussians of raw features: dict of xyz, f_dc, scale [n, 3], rotation [n, 4], opacity [n] (fp32)."""
+    lib = load()
+    _require_cuda(anchors, features, perturbation, rep)
+    for t in (anchors, features, perturbation, rep):
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError("to_gaussians takes contiguous fp32 tensors")
+    rows = anchors.shape[0]
+    if features.shape != (rows, per_anchor * 15) or perturbation.numel() != per_anchor * 3 or rep.numel() != 10:
+        raise ValueError("to_gaussians: shapes do not match")
+    n = rows * per_anchor
+    dev = anchors.device
+    out = {"xyz": torch.empty((n, 3), device=dev), "f_dc": torch.empty((n, 3), device=dev),
+           "scale": torch.empty((n, 3), device=dev), "rotation": torch.empty((n, 4), device=dev),
+           "opacity": torch.empty(n, device=dev)}
+    _check(lib.idolq_to_gaussians(_ptr(anchors), rows, _ptr(features), per_anchor, _ptr(perturbation), _ptr(rep),
+                                  _ptr(out["xyz"]), _ptr(out["f_dc"]), _ptr(out["scale"]), _ptr(out["rotation"]),
+                                  _ptr(out["opacity"]), _stream(dev)))
     return out

@@ -201,6 +201,14 @@ int idolq_rms_heads(void* x, int dtype, int64_t rows, int64_t ld, int64_t heads,
 int idolq_add_gated(void* x, int x_dtype, int64_t ldx, const void* h, int h_dtype, int64_t ldh, int64_t rows,
                     int64_t dim, const float* gate, void* stream);
 
+/* Raw Gaussian features [rows x per_anchor * 15] of anchors [rows x 3] -> activated Gaussians (rows * per_anchor of
+ * them): xyz, f_dc, scale [n x 3], rotation [n x 4] (unit quaternion, w first), opacity [n] (src/decoders.cpp:393-431
+ * to_gaussians). perturbation [per_anchor x 3]; rep[10] = perturbe, kernel, lr_xyz, lr_dc, lr_opacity, lr_scaling,
+ * lr_rotation, scale_offset, opacity_offset, base_offset_scale (all fp32). */
+int idolq_to_gaussians(const float* anchors, int64_t rows, const float* features, int64_t per_anchor,
+                       const float* perturbation, const float* rep, float* xyz, float* f_dc, float* scale,
+                       float* rotation, float* opacity, void* stream);
+
 /* The octree level embedding: out[i] = cos(((resolution * freqs[i]) * 2) * pi), out[half + i] = sin(same), fp32,
  * out [2 * half] (src/decoders.cpp:262-266). */
 int idolq_level_embed(float resolution, const float* freqs, int64_t half, float* out, void* stream);

@@ -104,6 +104,13 @@ def ref_lib():
         lib.ref_gelu_scalar.argtypes = [_f32p, _i64, _f32p]
         lib.ref_last_error.restype = ctypes.c_char_p
         lib.ref_set_quant_kernel.argtypes = [_int]
+        lib.ref_uniform_floats.argtypes = [ctypes.c_uint64, _i64, _f32p, _vp]
+        lib.ref_decoders_sample_anchors.argtypes = [_vp, _f32p, _int, _int, _int, ctypes.c_uint64, _f32p]
+        lib.ref_decoders_sample_anchors.restype = _int
+        lib.ref_decoders_to_gaussians.argtypes = [_vp, _f32p, _int, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p]
+        lib.ref_decoders_to_gaussians.restype = _int
+        lib.ref_write_gaussian_ply.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _i64, ctypes.c_char_p]
+        lib.ref_write_gaussian_ply.restype = _int
         lib.ref_rms_heads.argtypes = [_f32p, _int, _int, _int, _int, _f32p]
         lib.ref_add_gated.argtypes = [_f32p, _f32p, _int, _int, _f32p]
         lib.ref_decoders_open.argtypes = [ctypes.c_char_p]
@@ -431,6 +438,24 @@ class RefDecoders:
             raise RuntimeError(ref_lib().ref_last_error().decode())
         return out
 
+    def sample_anchors(self, cond, num_points, level, seed):
+        cond = _f32(cond)
+        out = np.empty((num_points, 3), np.float32)
+        if ref_lib().ref_decoders_sample_anchors(self._h, cond, cond.shape[0], num_points, level, seed, out):
+            raise RuntimeError(ref_lib().ref_last_error().decode())
+        return out
+
+    def to_gaussians(self, anchors, features):
+        anchors, features = _f32(anchors), _f32(features)
+        n = anchors.shape[0] * self.per_anchor
+        out = {"xyz": np.empty((n, 3), np.float32), "f_dc": np.empty((n, 3), np.float32),
+               "scale": np.empty((n, 3), np.float32), "rotation": np.empty((n, 4), np.float32),
+               "opacity": np.empty(n, np.float32)}
+        if ref_lib().ref_decoders_to_gaussians(self._h, anchors, anchors.shape[0], features, out["xyz"], out["f_dc"],
+                                               out["scale"], out["rotation"], out["opacity"]):
+            raise RuntimeError(ref_lib().ref_last_error().decode())
+        return out
+
     def gaussian_features(self, points, cond):
         points, cond = _f32(points), _f32(cond)
         out = np.empty((points.shape[0], self.per_anchor * 15), np.float32)
@@ -534,3 +559,18 @@ def q4_0_quantize(w):
     out[:, :2] = d.astype(np.float16).reshape(-1, 1).view(np.uint8)
     out[:, 2:] = q[:, :16] | (q[:, 16:] << 4)
     return out.reshape(-1)
+
+
+def ref_uniform_floats(seed, count):
+    """(floats, raw 64-bit outputs) of std::mt19937_64(seed) with std::uniform_real_distribution<float>(0, 1)."""
+    out = np.empty(count, np.float32)
+    raw = np.empty(count, np.uint64)
+    ref_lib().ref_uniform_floats(seed, count, out, raw.ctypes.data_as(ctypes.c_void_p))
+    return out, raw
+
+
+def ref_write_gaussian_ply(cloud, path):
+    c = {k: _f32(v) for k, v in cloud.items()}
+    if ref_lib().ref_write_gaussian_ply(c["xyz"], c["f_dc"], c["scale"], c["rotation"], c["opacity"],
+                                        c["opacity"].size, str(path).encode()):
+        raise RuntimeError(ref_lib().ref_last_error().decode())

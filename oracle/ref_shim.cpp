@@ -152,4 +152,49 @@ int ref_decoders_gaussian_features(void* d, const float* points, int rows, const
     return guarded([&] { static_cast<idol::Decoders*>(d)->gaussian_features(points, rows, cond, cond_rows, out); });
 }
 
+// The generator and distribution the reference's sampling uses (src/decoders.cpp:338-339): count uniform floats in
+// [0, 1) from std::mt19937_64(seed) through std::uniform_real_distribution<float>, and the raw 64-bit outputs.
+void ref_uniform_floats(std::uint64_t seed, std::int64_t count, float* out, std::uint64_t* raw) {
+    std::mt19937_64 rng(seed), rng2(seed);
+    std::uniform_real_distribution<float> uniform(0.0f, 1.0f);
+    for (std::int64_t i = 0; i < count; ++i) {
+        out[i] = uniform(rng);
+        if (raw) raw[i] = rng2();
+    }
+}
+
+// Decoders::sample_anchors (num_points x 3 into out), to_gaussians (anchors rows x 3, features rows x G*15 ->
+// xyz, f_dc, scale [n x 3], rotation [n x 4], opacity [n]) and write_gaussian_ply of such a cloud.
+int ref_decoders_sample_anchors(void* d, const float* cond, int cond_rows, int num_points, int level,
+                                std::uint64_t seed, float* out) {
+    return guarded([&] {
+        const std::vector<float> p = static_cast<idol::Decoders*>(d)->sample_anchors(cond, cond_rows, num_points,
+                                                                                     level, seed);
+        std::copy(p.begin(), p.end(), out);
+    });
+}
+int ref_decoders_to_gaussians(void* d, const float* anchors, int rows, const float* features, float* xyz,
+                              float* f_dc, float* scale, float* rotation, float* opacity) {
+    return guarded([&] {
+        const idol::GaussianCloud c = static_cast<idol::Decoders*>(d)->to_gaussians(anchors, rows, features);
+        std::copy(c.xyz.begin(), c.xyz.end(), xyz);
+        std::copy(c.f_dc.begin(), c.f_dc.end(), f_dc);
+        std::copy(c.scale.begin(), c.scale.end(), scale);
+        std::copy(c.rotation.begin(), c.rotation.end(), rotation);
+        std::copy(c.opacity.begin(), c.opacity.end(), opacity);
+    });
+}
+int ref_write_gaussian_ply(const float* xyz, const float* f_dc, const float* scale, const float* rotation,
+                           const float* opacity, std::int64_t n, const char* path) {
+    return guarded([&] {
+        idol::GaussianCloud c;
+        c.xyz.assign(xyz, xyz + n * 3);
+        c.f_dc.assign(f_dc, f_dc + n * 3);
+        c.scale.assign(scale, scale + n * 3);
+        c.rotation.assign(rotation, rotation + n * 4);
+        c.opacity.assign(opacity, opacity + n);
+        idol::write_gaussian_ply(c, path);
+    });
+}
+
 }  // extern "C"

@@ -237,3 +237,41 @@ def test_decoders_from_gguf_match_the_reference(tmp_path, quant):
             ref.close()
         print(f"{quant}: octree {norm_rel(a[0], r_oct):.3e} gaussian {norm_rel(a[1], r_gs):.3e}")
         assert norm_rel(a[0], r_oct) < 2e-5 and norm_rel(a[1], r_gs) < 2e-5
+
+
+def test_to_gaussians_sample_anchors_and_decode_match_the_reference():
+    # src/decoders.cpp:335-442 around the decoders: to_gaussians on the same features (libm-level differences only),
+    # the octree descent with this build's logits, and decode end to end
+    _needs_ref()
+    from decoders import GaussianCloud, write_gaussian_ply  # noqa: F401
+    dec = Decoders(GOLDEN / "decoders_small")
+    ref = O.RefDecoders(GOLDEN / "decoders_small")
+    rng = np.random.default_rng(41)
+    cond = rng.standard_normal((29, 16)).astype(np.float32)
+    anchors = rng.uniform(0, 1, (50, 3)).astype(np.float32)
+    feats = (2 * rng.standard_normal((50, 60))).astype(np.float32)
+    feats[0, :] = 30.0  # the softplus pass-through branch
+    K.set_quant_kernel(0)
+    O.ref_lib().ref_set_quant_kernel(0)
+    try:
+        cloud = dec.to_gaussians(_t(anchors), 50, _t(feats))
+        want = ref.to_gaussians(anchors, feats)
+        for key in ("xyz", "f_dc", "scale", "rotation", "opacity"):
+            got = getattr(cloud, key).cpu().numpy()
+            assert np.allclose(got, want[key], rtol=2e-6, atol=1e-7), key
+        for num_points, level, seed in ((64, 2, 3), (500, 4, 9)):
+            got = dec.sample_anchors(cond, 29, num_points, level, seed)
+            exp = ref.sample_anchors(cond, num_points, level, seed)
+            same = np.mean(np.all(got == exp, axis=1))
+            print(f"sample_anchors {num_points} points, level {level}: {same:.4f} identical")
+            assert got.shape == exp.shape and same == 1.0
+        c = dec.decode(cond, 29, 400, 3, 5)
+        assert c.size() == 400 and all(torch.isfinite(getattr(c, k)).all() for k in ("xyz", "scale", "opacity"))
+        pts = ref.sample_anchors(cond, 100, 3, 5)
+        rc = ref.to_gaussians(pts, ref.gaussian_features(pts, cond))
+        for key in ("xyz", "f_dc", "scale", "rotation", "opacity"):
+            assert norm_rel(getattr(c, key).cpu().numpy(), rc[key]) < 1e-4, key
+    finally:
+        K.set_quant_kernel(-1)
+        O.ref_lib().ref_set_quant_kernel(-1)
+        ref.close()
