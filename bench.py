@@ -224,24 +224,30 @@ DECODER_POINTS = 262144
 
 def run_decoder_mlp(args):
     """The decoders' tall-skinny per-point MLP (352 -> 256 -> 256 -> 64 Q8_0 with ReLU, fp32 64 -> 14 head) on 262144
-    points: ms per pass, GB/s of the bytes a fused pass must move (fp32 features, coordinates and outputs), TFLOP/s."""
+    points: ms per pass (one launch; the layer-by-layer route beside it), GB/s of the bytes a fused pass must move (fp32 features, coordinates and outputs), TFLOP/s."""
     import torch
     import decoder_mlp
 
     model = decoder_mlp.PointMLP(seed=0)
     feats, coords = decoder_mlp.inputs(DECODER_POINTS, seed=1)
-    for _ in range(3):
-        model.forward(feats, coords)
-    torch.cuda.synchronize()
-    reps = 20
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(reps):
-        model.forward(feats, coords)
-    stop.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(stop) / reps
-    out = {"decoder_mlp_ms": round(ms, 4), "decoder_mlp_points": DECODER_POINTS,
+
+    def timed(fn, reps=20):
+        for _ in range(3):
+            fn(feats, coords)
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            fn(feats, coords)
+        stop.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / reps
+
+    # one launch (idolq_point_mlp), and the six-launch layer-by-layer route for comparison
+    ms = timed(model.forward)
+    layers_ms = timed(model.forward_layers)
+    out = {"decoder_mlp_ms": round(ms, 4), "decoder_mlp_layers_ms": round(layers_ms, 4),
+           "decoder_mlp_points": DECODER_POINTS,
            "decoder_mlp_gbs": round(model.min_bytes(DECODER_POINTS) / (ms * 1e-3) / 1e9, 1),
            "decoder_mlp_tflops": round(model.flop(DECODER_POINTS) / (ms * 1e-3) / 1e12, 2)}
     return out, model

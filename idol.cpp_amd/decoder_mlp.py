@@ -14,6 +14,9 @@ On the GPU the activations between layers are bf16 (the Q8_0 linears run in DEQU
 The first layer's depth is padded from 352 to 384 with zero blocks (and zero input columns) so that the 256-wide layers
 read the tiled weight layout (256-column tiles); the padding adds exact zeros. The 64-wide third layer reads the GGUF
 row-major blocks, whose kernel tiles 128 (or 64) columns. All buffers are allocated once per point count.
+
+forward() runs all of it in one launch (idolq_point_mlp: 64 points per workgroup, the activations in LDS, the
+weights as the bf16 values of their Q8_0 blocks in MFMA fragment order), with the same roundings; forward_layers() is the six-launch route.
 """
 import torch
 
@@ -49,6 +52,10 @@ class PointMLP:
         w1pad = torch.cat([w1, torch.zeros((hidden, pad_blocks, 34), dtype=torch.uint8, device=device)], dim=1)
         self.wt = {"l1": L.tile_q8_0(w1pad.reshape(-1).contiguous(), hidden, self.k1pad),
                    "l2": L.tile_q8_0(self.w["l2"], hidden, hidden)}
+        # the fused kernel's operands: the bf16 values of the Q8_0 weights (the DEQUANT arithmetic's weights)
+        self._fusable = (feat, nfreq, hidden, mid) == (FEAT, NFREQ, HIDDEN, MID) and out <= 16
+        self.wv = {name: L.dequant(self.w[name], n, k, torch.bfloat16) for name, (n, k) in self.shape.items()}
+        self.wp = L.point_mlp_pack(self.wv["l1"], self.wv["l2"], self.wv["l3"]) if self._fusable else None
         self._m = None
 
     def _buffers(self, m):
@@ -70,7 +77,15 @@ class PointMLP:
         return self.x
 
     def forward(self, feats, coords):
-        """[m, 14] fp32 head outputs for fp32 features [m, 256] and coordinates [m, 3]."""
+        """[m, 14] fp32 head outputs for fp32 features [m, 256] and coordinates [m, 3]: one launch
+        (idolq_point_mlp) for the synthetic size, else the layer-by-layer route."""
+        if not self._fusable:
+            return self.forward_layers(feats, coords)
+        return L.point_mlp(feats, coords, self.freqs, self.wp[0], self.b["l1"], self.wp[1], self.b["l2"], self.wp[2],
+                           self.b["l3"], self.head_w, self.head_b)
+
+    def forward_layers(self, feats, coords):
+        """The same outputs layer by layer: embedding, three Q8_0 GEMMs, the fp32 head (six launches)."""
         x = self.embed(feats, coords)
         relu, dq = L.ACT_RELU, L.MODE_DEQUANT
         L.gemm(x, self.wt["l1"], self.hidden, bias=self.b["l1"], act=relu, mode=dq, out=self.h1, tiled=True)

@@ -43,6 +43,8 @@ _SIGNATURES = {
                                _i64, _i64, _vp]),
     "idolq_activation": (_int, [_vp, _int, _i64, _int, _vp]),
     "idolq_pos_embed": (_int, [_vp, _i64, _vp, _i64, _vp, _int, _i64, _vp]),
+    "idolq_point_mlp": (_int, [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp,
+                               _i64, _vp]),
     "idolq_copy2d": (_int, [_vp, _int, _i64, _vp, _int, _i64, _i64, _i64, _vp]),
     "idolq_gemm_f32": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _int, _vp, _i64, _vp]),
     "idolq_rms_heads": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _vp, _vp]),
@@ -307,6 +309,51 @@ def pos_embed(coords, freqs, out, ldo=None):
         ldo = _row_stride(out)
     _check(lib.idolq_pos_embed(_ptr(coords), rows, _ptr(freqs), freqs.numel(), _ptr(out), _code(out), ldo,
                                _stream(coords.device)))
+    return out
+
+
+def _point_mlp_fragments(w):
+    """[n, k] bf16 -> MFMA fragment order: fragment (n-tile t, 16-deep chunk c) is 1 KB at (t * k / 16 + c) KB, lane
+    l = 32 h + r holding row 32 t + r, depth 16 c + 8 h .. + 8 in its 16 bytes."""
+    n, k = w.shape
+    return w.reshape(n // 32, 32, k // 16, 2, 8).permute(0, 2, 3, 1, 4).contiguous().reshape(-1)
+
+
+def point_mlp_pack(w1, w2, w3):
+    """The fused per-point MLP's weight operands from the bf16 values of the three Q8_0 layers (w1 [256, 352],
+    w2 [256, 256], w3 [64, 256]): each in MFMA fragment order; w3's rows first permuted so that row 32 b + i is
+    feature 32 ((i / 4) % 2) + 16 b + 4 (i / 8) + i % 4 (each lane half then holds 32 consecutive features)."""
+    for w, shape in ((w1, (256, 352)), (w2, (256, 256)), (w3, (64, 256))):
+        if w.dtype != torch.bfloat16 or tuple(w.shape) != shape:
+            raise ValueError(f"weights must be bf16 {shape}")
+    i = torch.arange(32)
+    feat = 32 * ((i >> 2) & 1) + 4 * (i >> 3) + (i & 3)
+    order = torch.cat([feat, feat + 16]).to(w3.device)
+    return _point_mlp_fragments(w1), _point_mlp_fragments(w2), _point_mlp_fragments(w3[order])
+
+
+def point_mlp(feats, coords, freqs, w1, b1, w2, b2, w3, b3, wh, bh=None, out=None):
+    """The decoders' per-point MLP in one launch: fp32 features [m, 256] and coordinates [m, 3], a 16-frequency
+    sine/cosine embedding, three ReLU layers on bf16 weight values packed by point_mlp_pack (from w1 [256, 352],
+    w2 [256, 256], w3 [64, 256]; fp32 biases) and an fp32 head wh [nout, 64] (nout <= 16). Returns fp32 [m, nout]."""
+    lib = load()
+    dev = _require_cuda(feats, coords, freqs, w1, b1, w2, b2, w3, b3, wh, bh, out)
+    m = feats.shape[0]
+    for w, size in ((w1, 256 * 352), (w2, 256 * 256), (w3, 64 * 256)):
+        if w.dtype != torch.bfloat16 or w.numel() != size or not w.is_contiguous():
+            raise ValueError("weights must be the contiguous bf16 operands of point_mlp_pack")
+    for t in (feats, coords, freqs, b1, b2, b3, wh) + ((bh,) if bh is not None else ()):
+        if t.dtype != torch.float32:
+            raise ValueError("features, coordinates, frequencies, biases and the head are fp32")
+    if (feats.shape[1] != 256 or feats.stride(1) != 1 or not coords.is_contiguous() or tuple(coords.shape) != (m, 3)
+            or not (wh.is_contiguous() and wh.shape[1] == 64)):
+        raise ValueError("features [m, 256], contiguous coordinates [m, 3] and a contiguous head [nout, 64]")
+    nout = wh.shape[0]
+    if out is None:
+        out = torch.empty((m, nout), device=feats.device, dtype=torch.float32)
+    _check(lib.idolq_point_mlp(_ptr(feats), m, feats.stride(0), _ptr(coords), _ptr(freqs), freqs.numel(), _ptr(w1),
+                               _ptr(b1), _ptr(w2), _ptr(b2), _ptr(w3), _ptr(b3), _ptr(wh), _ptr(bh), nout, _ptr(out),
+                               out.stride(0), _stream(dev)))
     return out
 
 

@@ -164,6 +164,21 @@ int idolq_pos_embed(const float* coords, int64_t rows, const float* freqs, int64
 int idolq_linear_f32(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const float* w, int64_t n,
                      const float* bias, int act, void* y, int y_dtype, int64_t ldy, void* stream);
 
+/* The decoders' per-point MLP in one launch (the per-point heads of src/decoders.cpp:232-316, the embedding of
+ * src/decoders.cpp:215-230): x = [feats (256) | sin/cos embedding of coords (3 x nfreq x 2, nfreq = 16)],
+ * h1 = relu(x W1^T + b1) (256), h2 = relu(h1 W2^T + b2) (256), h3 = relu(h2 W3^T + b3) (64), y = h3 Wh^T + bh.
+ * feats [m x 256] fp32 (row stride ldf, a multiple of 4), coords [m x 3] fp32, freqs [16] fp32; w1 [256 x 352],
+ * w2 [256 x 256], w3 [64 x 256]: the bf16 values of Q8_0 weights (idolq_q8_0_dequant to bf16) in MFMA fragment
+ * order -- fragment (row tile t of 32 rows, 16-deep chunk c) is 1 KB at byte (t * k / 16 + c) * 1024, its 16-byte
+ * piece l = 32 h + r holding row 32 t + r, depth 16 c + 8 h .. + 8 -- with w3's rows first permuted so that row
+ * 32 b + i is feature 32 ((i / 4) % 2) + 16 b + 4 (i / 8) + i % 4 (idolq_lib.point_mlp_pack); biases fp32; wh [nout x 64] fp32 with 1 <= nout <= 16, bh NULL or [nout]; y [m x nout] fp32 (row stride ldy). The same
+ * arithmetic as the layer-by-layer route (idolq_pos_embed, three DEQUANT idolq_q8_0_gemm calls with ReLU,
+ * idolq_linear_f32): x and the hidden activations rounded to bf16, fp32 accumulation, the head's sums in
+ * idolq_linear_f32's order. feats, w1, w2, w3, b1 and b2 16-byte aligned. */
+int idolq_point_mlp(const float* feats, int64_t m, int64_t ldf, const float* coords, const float* freqs, int64_t nfreq,
+                    const void* w1, const float* b1, const void* w2, const float* b2, const void* w3, const float* b3,
+                    const float* wh, const float* bh, int64_t nout, float* y, int64_t ldy, void* stream);
+
 /* Copies a [rows x cols] block between dtypes and strides (a column slice of a wider row is a pointer offset). */
 int idolq_copy2d(const void* src, int src_dtype, int64_t lds, void* dst, int dst_dtype, int64_t ldd, int64_t rows,
                  int64_t cols, void* stream);

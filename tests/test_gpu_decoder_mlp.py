@@ -30,13 +30,46 @@ def cpu_forward(model, feats, coords):
     return O.gemm_dense(h, model.head_w.cpu().numpy(), model.head_b.cpu().numpy()), h
 
 
-def test_point_mlp_matches_cpu_chain():
+@pytest.mark.parametrize("route", ["fused", "layers"])
+def test_point_mlp_matches_cpu_chain(route):
     model = PointMLP(seed=3)
     feats, coords = inputs(2048, seed=4)
-    got = model.forward(feats, coords).cpu().numpy()
+    fn = model.forward if route == "fused" else model.forward_layers
+    got = fn(feats, coords).cpu().numpy()
     ref, _ = cpu_forward(model, feats.cpu().numpy(), coords.cpu().numpy())
     assert norm_rel(got, ref) < 2e-2
     assert norm_rel(got, ref) < 1e-2  # observed 5.4e-3: bf16 weight rounding, compounded over four layers
+
+
+@pytest.mark.parametrize("m,out", [(1, 14), (127, 14), (300, 14), (4096, 14), (1000, 16), (513, 1)])
+def test_fused_point_mlp_matches_the_layers(m, out):
+    # one launch against the six-launch route on the same weights: the same roundings, so the outputs agree up to
+    # the rare bf16 rounding flip of a hidden value whose fp32 sum differs in the last bits
+    print(f"fused point MLP m={m} out={out}", flush=True)
+    model = PointMLP(seed=m, out=out)
+    feats, coords = inputs(m, seed=m + 1)
+    fused = model.forward(feats, coords)
+    layers = model.forward_layers(feats, coords)
+    torch.cuda.synchronize()
+    assert fused.shape == (m, out) and torch.isfinite(fused).all()
+    assert norm_rel(fused.cpu().numpy(), layers.cpu().numpy()) < 2e-3
+    ref, _ = cpu_forward(model, feats.cpu().numpy(), coords.cpu().numpy())
+    assert norm_rel(fused.cpu().numpy(), ref) < 1e-2
+
+
+def test_fused_point_mlp_strided_features_and_empty():
+    model = PointMLP(seed=11)
+    feats, coords = inputs(300, seed=12)
+    wide = torch.zeros((300, 260), device="cuda")
+    wide[:, :256] = feats
+    a = model.forward(wide[:, :256], coords)
+    b = model.forward(feats, coords)
+    assert torch.equal(a, b)
+    empty = model.forward(feats[:0], coords[:0])
+    assert empty.shape == (0, 14)
+    with pytest.raises(ValueError):
+        L.point_mlp(feats, coords, model.freqs, model.wp[0].float(), model.b["l1"], model.wp[1], model.b["l2"],
+                    model.wp[2], model.b["l3"], model.head_w, model.head_b)
 
 
 @pytest.mark.parametrize("m,k,n", [(300, 64, 14), (1000, 100, 5), (257, 256, 32)])
