@@ -11,16 +11,17 @@
 // then bias and ReLU in fp32; the head sums each half of the depth in a sequential fp32 FMA chain and adds the two
 // halves, then the bias (the order of idolq_linear_f32).
 //
-// One workgroup (4 waves) takes 64 points, two workgroups per CU (one's loads and embedding overlap the other's
-// products); nothing but the fp32 inputs and outputs touches HBM:
-//   LDS X [64 x 352] bf16 (row stride 720 B: 16 B of padding keep the 16-byte operand reads conflict-free)
-//   LDS H [64 x 256] bf16 (row stride 528 B); h2 goes back into X's bytes with H's stride
-// Layers 1 and 2: wave w computes output features [64w, 64w + 64) of all 64 points, 2 x 2 accumulator tiles of
+// One workgroup (4 waves) takes 32 points, four workgroups per CU (their loads, embeddings and products overlap;
+// measured faster than 64 points with two per CU and 128 with one); nothing but the fp32 inputs and outputs
+// touches HBM:
+//   LDS X [32 x 352] bf16 (row stride 720 B: 16 B of padding keep the 16-byte operand reads conflict-free)
+//   LDS H [32 x 256] bf16 (row stride 528 B); h2 goes back into X's bytes with H's stride
+// Layers 1 and 2: wave w computes output features [64w, 64w + 64) of the 32 points, 2 accumulator tiles of
 // v_mfma_f32_32x32x16_bf16 in the transposed form D = W X^T (D rows are output features, columns points), point
 // operands from LDS, weight operands from global memory (L2-resident) in MFMA fragment order: fragment (n-tile t,
 // 16-deep chunk c) is 1 KB at (t K / 16 + c) KB, lane l = 32 h + r holding row 32 t + r, depth 16 c + 8 h .. + 8,
 // so one wave's operand load is 1 KB of consecutive bytes.
-// Layer 3 and the head: waves 0 and 1 take points [32w, 32w + 32) and all 64 features; the weight rows are
+// Layer 3 and the head: wave 0 takes the 32 points and all 64 features; the weight rows are
 // permuted (row 32 b + i is feature 32 ((i / 4) % 2) + 16 b + 4 (i / 8) + i % 4) so that the lane halves of a point
 // hold its features 0..31 and 32..63 in ascending order, and the head runs on those registers.
 #include <hip/hip_runtime.h>
@@ -32,13 +33,13 @@ using namespace idolq;
 
 namespace {
 
-constexpr int kPoints = 64, kThreads = 256, kTiles = kPoints / 32;
+constexpr int kPoints = 32, kThreads = 256, kTiles = kPoints / 32;
 constexpr int kFeat = 256, kFreq = 16, kK1 = kFeat + 6 * kFreq, kHidden = 256, kMid = 64, kMaxOut = 16;
 constexpr int kXStride = kK1 * 2 + 16;      // 720 bytes
 constexpr int kHStride = kHidden * 2 + 16;  // 528 bytes
 constexpr int kXBytes = kPoints * kXStride, kHBytes = kPoints * kHStride;
 constexpr int kLds = kXBytes + kHBytes;
-static_assert(kLds <= 81920, "LDS budget: two workgroups per CU");
+static_assert(4 * kLds <= 163840, "LDS budget: four workgroups per CU");
 static_assert(kXBytes >= kHBytes, "h2 reuses X's bytes");
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -96,7 +97,7 @@ __device__ __forceinline__ void wide_layer(const char* in, int in_stride, const 
     }
 }
 
-__global__ __launch_bounds__(kThreads, 2) void point_mlp_kernel(const float* __restrict__ feats, int64_t m, int64_t ldf,
+__global__ __launch_bounds__(kThreads, 3) void point_mlp_kernel(const float* __restrict__ feats, int64_t m, int64_t ldf,
                                                              const float* __restrict__ coords,
                                                              const float* __restrict__ freqs,
                                                              const __bf16* __restrict__ w1, const float* __restrict__ b1,

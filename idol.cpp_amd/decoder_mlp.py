@@ -15,7 +15,7 @@ The first layer's depth is padded from 352 to 384 with zero blocks (and zero inp
 read the tiled weight layout (256-column tiles); the padding adds exact zeros. The 64-wide third layer reads the GGUF
 row-major blocks, whose kernel tiles 128 (or 64) columns. All buffers are allocated once per point count.
 
-forward() runs all of it in one launch (idolq_point_mlp: 64 points per workgroup, the activations in LDS, the
+forward() runs all of it in one launch (idolq_point_mlp: 32 points per workgroup, the activations in LDS, the
 weights as the bf16 values of their Q8_0 blocks in MFMA fragment order), with the same roundings; forward_layers() is the six-launch route.
 """
 import torch
