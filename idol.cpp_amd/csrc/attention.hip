@@ -8,7 +8,9 @@
 // raised only when a tile exceeds it by more than 2^8 in probability, so most tiles skip rescaling. The probabilities
 // stay in registers and become, converted to fp16, the B operand of O^T = V^T * P^T (the row sums are taken from the
 // same fp16 values with dot2); the MFMA's k order is permuted to the order in which the score accumulator holds the
-// keys, and the V^T operand is read in that same order.
+// keys, and the V^T operand is read in that same order. bf16 values of V beyond fp16's range (|v| >= 65504) are
+// staged scaled by a power of two per tile and the tile's product is scaled back exactly, so the fp16 P * V never
+// overflows where the reference's fp32 attention does not.
 //
 // attn_f32_mfma (fp32 inputs, head_dim 32 or 64, 16-byte aligned rows): fp32 matrix cores for both products, the key
 // range split over the 4 waves of a 32-query workgroup; the reference's float attention surface at fp32 accuracy.
@@ -101,14 +103,22 @@ __global__ __launch_bounds__(256) void attn_mfma_hd64(AttnParams p) {
     float mc = -INFINITY, l_part = 0.0f;
     const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
 
+    // bf16 V beyond the fp16 range: a tile holding |v| >= 65504 is staged as fp16(v * 2^-e), exactly scaled by the
+    // power of two that brings its largest magnitude below 2^15, and its P * V is added as 2^e (2^-e o + P V')
+    // (exact scalings); other tiles, and every fp16 input, take the plain fp16 V^T.
+    constexpr bool kWideV = std::is_same<T, __bf16>::value;
+    __shared__ uint32_t vote[4];
+
     // one 64-key tile; MASK: the last tile, which holds fewer than 64 keys; FIRST: the first tile, which sets mc
     auto tile = [&](int64_t j0, auto mask_tag, auto first_tag) __attribute__((always_inline)) {
         constexpr bool MASK = decltype(mask_tag)::value, FIRST = decltype(first_tag)::value;
         __syncthreads();
         // Stage K [key][d] and V^T [d][key] (fp16): thread t takes keys 2 (t / 8) and 2 (t / 8) + 1, d chunk
         // 8 (t % 8); V^T gets one (key, key + 1) pair per d and dword store.
+        const int kp = threadIdx.x >> 3, part = threadIdx.x & 7;
+        uint32_t v0[4], v1[4];
+        bool big = false;
         {
-            const int kp = threadIdx.x >> 3, part = threadIdx.x & 7;
             uint4 kr[2], vr[2];
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
@@ -121,21 +131,53 @@ __global__ __launch_bounds__(256) void attn_mfma_hd64(AttnParams p) {
                 }
                 *reinterpret_cast<uint4*>(k_lds + (2 * kp + i) * kKPitch + 8 * part) = kr[i];
             }
-            const uint32_t v0[4] = {vr[0].x, vr[0].y, vr[0].z, vr[0].w}, v1[4] = {vr[1].x, vr[1].y, vr[1].z, vr[1].w};
+            v0[0] = vr[0].x, v0[1] = vr[0].y, v0[2] = vr[0].z, v0[3] = vr[0].w;
+            v1[0] = vr[1].x, v1[1] = vr[1].y, v1[2] = vr[1].z, v1[3] = vr[1].w;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const uint16_t b0 = (uint16_t)(v0[e >> 1] >> (16 * (e & 1))), b1 = (uint16_t)(v1[e >> 1] >> (16 * (e & 1)));
                 f16x2 pair;
-                if (std::is_same<T, _Float16>::value) {
+                if constexpr (!kWideV) {
                     pair = f16x2{__builtin_bit_cast(_Float16, b0), __builtin_bit_cast(_Float16, b1)};
                 } else {
                     const f32x2 f = {bf16_bits_to_float(b0), bf16_bits_to_float(b1)};
+                    big = big || fabsf(f.x) >= 65504.0f || fabsf(f.y) >= 65504.0f;
                     pair = __builtin_convertvector(f, f16x2);
                 }
                 *reinterpret_cast<f16x2*>(vt_lds + (8 * part + e) * kVPitch + 2 * kp) = pair;
             }
         }
-        __syncthreads();
+        int vexp = 0;  // this tile's V^T holds fp16(v * 2^-vexp)
+        if constexpr (kWideV) {
+            const uint32_t wave_big = __builtin_amdgcn_ballot_w64(big) != 0 ? 1u : 0u;  // every lane takes part
+            if (lane == 0) vote[wave] = wave_big;
+            __syncthreads();
+            if ((vote[0] | vote[1] | vote[2] | vote[3]) != 0) {  // workgroup-uniform; rare
+                // the largest exponent field among the tile's values (bf16 bits 14..7)
+                uint32_t eb = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    eb = max(eb, max(max(v0[e] & 0x7f80u, (v0[e] >> 16) & 0x7f80u), max(v1[e] & 0x7f80u, (v1[e] >> 16) & 0x7f80u)));
+#pragma unroll
+                for (int off = 32; off > 0; off >>= 1) eb = max(eb, (uint32_t)__shfl_xor((int)eb, off));
+                __syncthreads();  // every wave has read the vote
+                if (lane == 0) vote[wave] = eb;
+                __syncthreads();
+                eb = max(max(vote[0], vote[1]), max(vote[2], vote[3]));
+                // |v| < 2^(E + 1), E = (eb >> 7) - 127 >= 15: scaled by 2^-(E - 14) every value is below 2^15
+                vexp = (int)(eb >> 7) - 127 - 14;
+                const float down = __builtin_bit_cast(float, (uint32_t)(127 - vexp) << 23);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint16_t b0 = (uint16_t)(v0[e >> 1] >> (16 * (e & 1))), b1 = (uint16_t)(v1[e >> 1] >> (16 * (e & 1)));
+                    const f32x2 f = {bf16_bits_to_float(b0) * down, bf16_bits_to_float(b1) * down};
+                    *reinterpret_cast<f16x2*>(vt_lds + (8 * part + e) * kVPitch + 2 * kp) = __builtin_convertvector(f, f16x2);
+                }
+                __syncthreads();
+            }
+        } else {
+            __syncthreads();
+        }
 
         // S^T for 64 keys: two 32-key sub-tiles, 4 MFMAs each over d.
         f32x16 s[2];
@@ -187,6 +229,13 @@ __global__ __launch_bounds__(256) void attn_mfma_hd64(AttnParams p) {
 
         // O^T += V^T * P^T over 4 chunks of 16 keys. Chunk (st, kc) uses accumulator elements r = 8 kc + e of
         // sub-tile st; slot 8 * half + e of the MFMA's k holds key st*32 + 16 kc + 8 (e / 4) + 4 half + e % 4.
+        if (kWideV && vexp != 0) {
+            const float down = __builtin_bit_cast(float, (uint32_t)(127 - vexp) << 23);
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[t][r] *= down;
+        }
 #pragma unroll
         for (int st = 0; st < 2; ++st)
 #pragma unroll
@@ -212,6 +261,13 @@ __global__ __launch_bounds__(256) void attn_mfma_hd64(AttnParams p) {
                     o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pf, o[t], 0, 0, 0);
                 }
             }
+        if (kWideV && vexp != 0) {
+            const float up = __builtin_bit_cast(float, (uint32_t)(127 + vexp) << 23);
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[t][r] *= up;
+        }
     };
     const int64_t full_end = p.lk / kBKV * kBKV;
     if (full_end == 0) {

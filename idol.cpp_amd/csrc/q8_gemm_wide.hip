@@ -54,8 +54,9 @@ constexpr int kWideThreads = 256;  // 4 waves
 // workgroup. A tile whose stages fall into several ranges is finished by the part that arrives last: a part that
 // finds the others already counted keeps its sum in registers; otherwise it stores its fp32 partial tile in its slot
 // of `part` (device-coherent stores) and counts itself in count[first range of the tile]. The part that sees the
-// count complete adds the stored partial tiles to its own (in range order), runs the epilogue and clears the count
-// for the next launch. Nobody waits for anybody, so the workgroups need not be resident together.
+// count complete sums the parts in range order, left to right, its own registers taking its range's place (so the
+// result is the same whichever part finishes), runs the epilogue and clears the count for the next launch. Nobody
+// waits for anybody, so the workgroups need not be resident together.
 struct WideSplit {
     int G;        // workgroups
     int dp;       // tiles taken whole
@@ -481,23 +482,42 @@ __global__ __launch_bounds__(kWideThreads) void q8_wide_kernel(GemmParams p, Wid
                     finish = arrivals == last - first;
                 }
                 if (finish) {
-                    // every other part is stored: add them (range order), two accumulator tiles per batch of loads
-                    for (int c = first; c <= last; ++c) {
-                        if (c == r) continue;
-                        const int off = (2 * c + (t0 > begin_of(c) ? 1 : 0)) * kSlot + tid * 16;
+                    // every other part is stored: the tile's sum is part first + part first + 1 + ... + part last,
+                    // added left to right whichever part finishes (this part's own sum enters at its range's
+                    // position), so the result does not depend on the order of arrival. Eight uint4 pieces of the
+                    // accumulators per batch: the running sum of a batch lives in t, the batch's loads in v.
+                    auto slot_off = [&](int c) __attribute__((always_inline)) {
+                        return (2 * c + (t0 > begin_of(c) ? 1 : 0)) * kSlot + tid * 16;
+                    };
 #pragma unroll
-                        for (int q0 = 0; q0 < kQ; q0 += 8) {
-                            i32x4 v[8];
+                    for (int q0 = 0; q0 < kQ; q0 += 8) {
+                        f32x4 t[8];
+                        auto own = [&](int q) __attribute__((always_inline)) {
+                            const f32x16& a = acc[((q0 + q) >> 2) / CT][((q0 + q) >> 2) % CT];
+                            const int e0 = 4 * ((q0 + q) & 3);
+                            return f32x4{a[e0], a[e0 + 1], a[e0 + 2], a[e0 + 3]};
+                        };
+                        for (int c = first; c <= last; ++c) {
+                            f32x4 v[8];
+                            if (c == r) {
 #pragma unroll
-                            for (int q = 0; q < 8; ++q)
-                                v[q] = __builtin_amdgcn_raw_buffer_load_b128(prs, off + (q0 + q) * 4096, 0, kCoherent);
+                                for (int q = 0; q < 8; ++q) v[q] = own(q);
+                            } else {
+                                const int off = slot_off(c);
 #pragma unroll
-                            for (int q = 0; q < 8; ++q) {
-                                f32x16& a = acc[((q0 + q) >> 2) / CT][((q0 + q) >> 2) % CT];
-                                const f32x4 f = __builtin_bit_cast(f32x4, v[q]);
-#pragma unroll
-                                for (int e = 0; e < 4; ++e) a[4 * ((q0 + q) & 3) + e] += f[e];
+                                for (int q = 0; q < 8; ++q)
+                                    v[q] = __builtin_bit_cast(
+                                        f32x4, __builtin_amdgcn_raw_buffer_load_b128(prs, off + (q0 + q) * 4096, 0, kCoherent));
                             }
+#pragma unroll
+                            for (int q = 0; q < 8; ++q) t[q] = c == first ? v[q] : t[q] + v[q];
+                        }
+#pragma unroll
+                        for (int q = 0; q < 8; ++q) {
+                            f32x16& a = acc[((q0 + q) >> 2) / CT][((q0 + q) >> 2) % CT];
+                            const int e0 = 4 * ((q0 + q) & 3);
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) a[e0 + e] = t[q][e];
                         }
                     }
                     if (tid == 0) __hip_atomic_store(sp.count + first, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

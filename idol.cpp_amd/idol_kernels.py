@@ -142,6 +142,8 @@ def pack_panel(codes, scales, mins, bits, group):
     return np.ascontiguousarray(blob).reshape(-1)
 
 
+# ---- host restatement of the panel layout: the writers (tools/idolq.py:137-170 order) and loaders that hold their
+# weights on the host (device="cpu"); on the GPU the blob is converted by idolq_panel_to_q8_0 / idolq_panel_expand_f32.
 def panel_is_symmetric(scales, mins, bits):
     """True when every minimum is -2^(bits-1) * scale: the panel holds fp32(scale) * (code - 2^(bits-1))."""
     return bool(np.all(mins == -float(1 << (bits - 1)) * scales))
@@ -183,13 +185,23 @@ def quantized_linear(blob, bias, out, in_, bits, group, device="cuda"):
     npanels = (out + K_COLS - 1) // K_COLS
     if blob.size != npanels * quant_panel_bytes(in_, bits, group):
         raise ValueError("a quantized blob has the wrong size for its shape")
-    codes, scales, mins = unpack_panel(blob, out, in_, bits, group)
-    if panel_is_symmetric(scales, mins, bits):
-        q8 = torch.from_numpy(panel_to_q8_0(blob, out, in_, bits, group)).to(device)
-        layer = q8_0_linear(q8, bias, out, in_, device=device)
+    if torch.device(device).type == "cuda":
+        # on the device: the blocks when every group's minimum is exact (checked by the kernel), else fp32 values
+        dev_blob = torch.from_numpy(np.ascontiguousarray(blob)).to(device)
+        q8, inexact = L.panel_to_q8_0(dev_blob, out, in_, bits, group)
+        if int(inexact.item()) == 0:
+            layer = q8_0_linear(q8, bias, out, in_, device=device)
+        else:
+            w = L.panel_expand_f32(dev_blob, out, in_, bits, group)
+            layer = PackedLinear(out, in_, None, _padded_bias(bias, out, device), weight=w)
     else:
-        w = torch.from_numpy(panel_values(blob, out, in_, bits, group)).to(device)
-        layer = PackedLinear(out, in_, None, _padded_bias(bias, out, device), weight=w)
+        codes, scales, mins = unpack_panel(blob, out, in_, bits, group)
+        if panel_is_symmetric(scales, mins, bits):
+            q8 = torch.from_numpy(panel_to_q8_0(blob, out, in_, bits, group)).to(device)
+            layer = q8_0_linear(q8, bias, out, in_, device=device)
+        else:
+            w = torch.from_numpy(panel_values(blob, out, in_, bits, group)).to(device)
+            layer = PackedLinear(out, in_, None, _padded_bias(bias, out, device), weight=w)
     layer.qbits, layer.qgroup = bits, group
     return layer
 

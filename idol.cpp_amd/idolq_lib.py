@@ -54,6 +54,9 @@ _SIGNATURES = {
     "idolq_to_gaussians": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "idolq_blocks_dequant": (_int, [_vp, _int, _i64, _i64, _vp, _int, _vp]),
     "idolq_q4_0_to_q8_0": (_int, [_vp, _i64, _i64, _vp, _vp]),
+    "idolq_panel_bytes": (_i64, [_i64, _i64, _int, _int]),
+    "idolq_panel_expand_f32": (_int, [_vp, _i64, _i64, _i64, _int, _int, _vp, _i64, _vp]),
+    "idolq_panel_to_q8_0": (_int, [_vp, _i64, _i64, _i64, _int, _int, _vp, _vp, _vp]),
 }
 
 _lib = None
@@ -134,14 +137,20 @@ _split_workspaces = {}
 
 
 def _split_workspace(device, nbytes):
-    """The zero-filled DEQUANT workspace of a device (partial tiles and flags of the split k stages), kept for the
-    process: the library leaves it ready for the next call. Calls on one device share it, so they must not overlap
-    (one stream)."""
-    ws = _split_workspaces.get(device)
+    """The zero-filled DEQUANT workspace (tile counters, then partial tiles of the split k stages) of the current
+    stream of a device, kept for the process: the library leaves it ready for the next call. Each stream has its own,
+    so calls on different streams never share counters; calls on one stream run one after another."""
+    key = (device, torch.cuda.current_stream(device).cuda_stream)
+    ws = _split_workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(nbytes, device=device, dtype=torch.uint8)
-        _split_workspaces[device] = ws
+        _split_workspaces[key] = ws
     return ws
+
+
+def split_workspace_of(device):
+    """The split workspace of the current stream of `device` (None before the first split call on it)."""
+    return _split_workspaces.get((device, torch.cuda.current_stream(device).cuda_stream))
 
 
 def gemm(x, w, n_total, n_offset=0, n=None, bias=None, residual=None, act=ACT_NONE, mode=MODE_AUTO, flags=0,
@@ -349,8 +358,15 @@ def point_mlp(feats, coords, freqs, w1, b1, w2, b2, w3, b3, wh, bh=None, out=Non
             or not (wh.is_contiguous() and wh.shape[1] == 64)):
         raise ValueError("features [m, 256], contiguous coordinates [m, 3] and a contiguous head [nout, 64]")
     nout = wh.shape[0]
+    for t, size, name in ((b1, 256, "b1"), (b2, 256, "b2"), (b3, 64, "b3"), (freqs, 16, "freqs")) + \
+            (((bh, nout, "bh"),) if bh is not None else ()):
+        if t.dim() != 1 or t.numel() != size or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous vector of {size} values")
     if out is None:
         out = torch.empty((m, nout), device=feats.device, dtype=torch.float32)
+    elif (out.dtype != torch.float32 or out.dim() != 2 or tuple(out.shape) != (m, nout)
+          or (nout > 1 and out.stride(1) != 1) or out.stride(0) < nout):
+        raise ValueError(f"out must be fp32 [{m}, {nout}] with unit column stride")
     _check(lib.idolq_point_mlp(_ptr(feats), m, feats.stride(0), _ptr(coords), _ptr(freqs), freqs.numel(), _ptr(w1),
                                _ptr(b1), _ptr(w2), _ptr(b2), _ptr(w3), _ptr(b3), _ptr(wh), _ptr(bh), nout, _ptr(out),
                                out.stride(0), _stream(dev)))
@@ -475,3 +491,40 @@ def to_gaussians(anchors, features, per_anchor, perturbation, rep):
                                   _ptr(out["xyz"]), _ptr(out["f_dc"]), _ptr(out["scale"]), _ptr(out["rotation"]),
                                   _ptr(out["opacity"]), _stream(dev)))
     return out
+
+
+def panel_bytes(out, in_, bits, group):
+    """Bytes of a native panel blob (0 for an invalid bit width or group)."""
+    return int(load().idolq_panel_bytes(out, in_, bits, group))
+
+
+def panel_expand_f32(blob, out, in_, bits, group, w=None):
+    """fp32 [out, in_] values fma(code, scale, min) of a panel blob held on the device (uint8)."""
+    lib = load()
+    dev = _require_cuda(blob, w)
+    if blob.dtype != torch.uint8 or not blob.is_contiguous():
+        raise ValueError("a panel blob is a contiguous uint8 tensor")
+    if w is None:
+        w = torch.empty((out, in_), device=dev, dtype=torch.float32)
+    elif w.dtype != torch.float32 or tuple(w.shape) != (out, in_) or (in_ > 1 and w.stride(1) != 1):
+        raise ValueError(f"w must be fp32 [{out}, {in_}] with unit column stride")
+    _check(lib.idolq_panel_expand_f32(_ptr(blob), blob.numel(), out, in_, bits, group, _ptr(w),
+                                      max(w.stride(0), in_), _stream(dev)))
+    return w
+
+
+def panel_to_q8_0(blob, out, in_, bits, group, inexact=None):
+    """(Q8_0 blocks, inexact) of a panel blob on the device: the blocks hold the panel's values when the device
+    int32 `inexact` (zeroed here unless passed in) ends at zero."""
+    lib = load()
+    dev = _require_cuda(blob, inexact)
+    if blob.dtype != torch.uint8 or not blob.is_contiguous():
+        raise ValueError("a panel blob is a contiguous uint8 tensor")
+    if in_ % 32:
+        raise ValueError("the quantization group must be a multiple of 32 that divides the input size")
+    q8 = torch.empty(out * (in_ // 32) * Q8_0_BYTES, device=dev, dtype=torch.uint8)
+    if inexact is None:
+        inexact = torch.zeros(1, device=dev, dtype=torch.int32)
+    _check(lib.idolq_panel_to_q8_0(_ptr(blob), blob.numel(), out, in_, bits, group, _ptr(q8), _ptr(inexact),
+                                   _stream(dev)))
+    return q8, inexact

@@ -197,6 +197,29 @@ int idolq_blocks_dequant(const uint8_t* w, int kind, int64_t n, int64_t k, void*
  * computes the Q4_0 layer's products (the Q4_0 case of tools/idol_triton.py:48-60). */
 int idolq_q4_0_to_q8_0(const uint8_t* w, int64_t n, int64_t k, uint8_t* out, void* stream);
 
+/* ---- Native quantized panels (src/kernels.hpp:33-51), the reference's own weight format for gemm_packed. ---- */
+
+/* Bytes of the panel blob of an [out x in] layer quantized with `bits` in groups of `group` k values:
+ * ceil(out / 16) * (in / group) * (64 + 2 * group * bits); 0 when bits is not 2, 3, 4, 5, 6 or 8 or group is not a
+ * multiple of 32 dividing in. Replaces src/kernels.cpp:512-514 quant_panel_bytes (times the panel count). */
+int64_t idolq_panel_bytes(int64_t out, int64_t in, int bits, int group);
+
+/* w[r * ldw + c] = fma(code, scale, min) in fp32 for every weight of a panel blob (device memory, blob_bytes long):
+ * the values of the reference's dequantizer, src/kernels.cpp:167-209 dequant8 / dequant_chunk and :535-550
+ * dequantize_linear, bit for bit. The argument checks and messages are those of src/kernels.cpp:516-533
+ * quantized_linear (bits, group, blob size). */
+int idolq_panel_expand_f32(const uint8_t* blob, int64_t blob_bytes, int64_t out, int64_t in, int bits, int group,
+                           float* w, int64_t ldw, void* stream);
+
+/* A panel blob whose every minimum is -2^(bits-1) * scale holds exactly fp32(scale) * (code - 2^(bits-1)); this
+ * writes those values as GGUF Q8_0 blocks q8 (out * in / 32 * 34 bytes, 2-byte aligned): d = the group's fp16 scale,
+ * q = code - 2^(bits-1), the inverse of tools/gguf_to_decoder.py:16-40 native_blob for any width and group. Groups
+ * whose minimum is not exact are counted into the device int32 *inexact (added to, so zero it first); where it ends
+ * non-zero the blocks do not hold the panel's values and the layer is expanded with idolq_panel_expand_f32 instead.
+ * Same argument checks as idolq_panel_expand_f32. */
+int idolq_panel_to_q8_0(const uint8_t* blob, int64_t blob_bytes, int64_t out, int64_t in, int bits, int group,
+                        uint8_t* q8, int32_t* inexact, void* stream);
+
 /* ---- The real decoders' operators (src/decoders.cpp), fp32 surface, in the reference's operation order. ---- */
 
 /* Dense fp32 GEMM of any shape: y[m x n] = act(x[m x k] * w^T + bias + residual), w [n x k] row-major, bias NULL or

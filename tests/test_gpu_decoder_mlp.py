@@ -67,9 +67,23 @@ def test_fused_point_mlp_strided_features_and_empty():
     assert torch.equal(a, b)
     empty = model.forward(feats[:0], coords[:0])
     assert empty.shape == (0, 14)
-    with pytest.raises(ValueError):
-        L.point_mlp(feats, coords, model.freqs, model.wp[0].float(), model.b["l1"], model.wp[1], model.b["l2"],
-                    model.wp[2], model.b["l3"], model.head_w, model.head_b)
+    args = [feats, coords, model.freqs, model.wp[0], model.b["l1"], model.wp[1], model.b["l2"], model.wp[2],
+            model.b["l3"], model.head_w, model.head_b]
+    bad = [(3, model.wp[0].float()),            # fp32 weights
+           (4, model.b["l1"][:255]),            # short bias (would be read past its end on the device)
+           (8, model.b["l3"].repeat(2)),        # long b3
+           (10, model.head_b[:3]),              # short head bias
+           (2, model.freqs[:8])]                # 8 frequencies
+    for i, t in bad:
+        call = list(args)
+        call[i] = t
+        with pytest.raises(ValueError):
+            L.point_mlp(*call)
+    for out in (torch.empty((300, 14), device="cuda", dtype=torch.bfloat16),   # wrong dtype
+                torch.empty((299, 14), device="cuda"),                         # too few rows
+                torch.empty((14, 300), device="cuda").T):                      # column stride 300
+        with pytest.raises(ValueError):
+            L.point_mlp(*args, out=out)
 
 
 @pytest.mark.parametrize("m,k,n", [(300, 64, 14), (1000, 100, 5), (257, 256, 32)])

@@ -182,3 +182,57 @@ def test_attention_fp32_matrix_cores_match_the_reference(hd, lq, lk, heads, batc
         pr = np.exp(s - s.max(axis=1, keepdims=True))
         o64 = (pr / pr.sum(axis=1, keepdims=True)) @ v[:, :hd].astype(np.float64)
         assert np.max(np.abs(got[bi, :, :hd] - o64)) < 2e-5
+
+
+def test_self_attention_seq4096_sample():
+    # config-2 self-attention at its real shape: batch 2 x 4096 tokens, 24 heads of 64, q/k/v column slices of one
+    # [8192, 4608] bf16 projection buffer; 128 sampled queries of each batch against the oracle over all 4096 keys
+    rng = np.random.default_rng(25)
+    B, S, heads, hd = 2, 4096, 24, 64
+    D = heads * hd
+    qkv = to_dev(rng.normal(0, 1, (B * S, 3 * D)).astype(np.float32)).bfloat16()
+    out = torch.empty((B * S, D), device=DEV, dtype=torch.bfloat16)
+    L.attention(qkv[:, :D], qkv[:, D:2 * D], qkv[:, 2 * D:], B, S, S, heads, hd, 3 * D, 3 * D, S * 3 * D, S * 3 * D,
+                out, D, S * D)
+    host = qkv.float().cpu().numpy()
+    got = out.float().cpu().numpy()
+    rows = np.arange(5, S, 32)
+    for b in range(B):
+        blk = host[b * S:(b + 1) * S]
+        ref = O.attention(np.ascontiguousarray(blk[rows, :D]), blk[:, D:2 * D], blk[:, 2 * D:], len(rows), S, D, D,
+                          heads, hd)
+        assert norm_rel(got[b * S + rows], torch.from_numpy(ref).bfloat16().float().numpy()) < 1e-3, b
+    assert np.isfinite(got).all()
+
+
+def test_attention_bf16_values_beyond_fp16_range():
+    # bf16 V holds values far beyond fp16's 65504 (the reference's fp32 attention takes them): the tiles that hold
+    # them are staged with an exact power-of-two scale, so the output stays finite and within the 16-bit bar, with
+    # large scores (peaky softmax) as well. Head 1 holds ordinary values: its workgroups take the plain path and
+    # give the same bits as a call where no head holds large values.
+    rng = np.random.default_rng(26)
+    lq, lk, heads, hd = 200, 300, 2, 64
+    dim = heads * hd
+    q = rng.normal(0, 2.5, (lq, dim)).astype(np.float32)
+    k = rng.normal(0, 2.5, (lk, dim)).astype(np.float32)
+    v = rng.normal(0, 1, (lk, dim)).astype(np.float32)
+    big = v.copy()
+    big[64:128, :hd] *= 1e5           # tile 1: |v| up to ~4e5
+    big[130, 7] = 3.0e30              # tile 2: one huge value
+    big[256:300, :hd] *= -7e4         # the partial last tile
+    qd, kd = to_dev(q).bfloat16(), to_dev(k).bfloat16()
+    outs = []
+    for vals in (v, big):
+        vd = to_dev(vals).bfloat16()
+        out = torch.empty((lq, dim), device=DEV, dtype=torch.float32)
+        L.attention(qd, kd, vd, 1, lq, lk, heads, hd, dim, dim, 0, 0, out, dim, 0)
+        outs.append(out)
+        ref = O.attention(qd.float().cpu().numpy(), kd.float().cpu().numpy(), vd.float().cpu().numpy(), lq, lk, dim,
+                          dim, heads, hd)
+        got = out.cpu().numpy()
+        assert np.isfinite(got).all()
+        for h in range(heads):
+            cols = slice(h * hd, (h + 1) * hd)
+            assert norm_rel(got[:, cols], ref[:, cols]) < 1e-3, h
+    assert torch.equal(outs[0][:, hd:], outs[1][:, hd:])
+    assert float(outs[1][:, :hd].abs().max()) > 1e5
