@@ -18,6 +18,7 @@
 #include "q8_gemm.h"
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 namespace idolq {
@@ -882,4 +883,64 @@ extern "C" int idolq_q8_0_block_dots(const int8_t* qa, int64_t m, int64_t k, con
     p.dots = dots;
     const bool w4 = p.row_bytes % 4 == 0 && (reinterpret_cast<uintptr_t>(p.w) & 3) == 0;
     return launch_int8<128, 128, true>(p, w4, static_cast<hipStream_t>(stream));
+}
+
+// ------------------------------------------------------------------------------------------------ no-allocation GEMM
+// idolq_q8_0_gemm_noalloc takes its scratch (the INT8 mode's quantized activations and scales) from this array. Each
+// device holds its own copy for the life of the process; host code reaches it only through the address
+// hipGetSymbolAddress returns on that device (kept in noalloc_scratch below), never through the array's name.
+namespace {
+
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+
+// The device address of `scratch` on the current device, looked up once per device (with that device current).
+void* noalloc_scratch(int* rc) {
+    static std::mutex mu;
+    static void* addr[kMaxDevices] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        *rc = fail(IDOLQ_ELAUNCH, "no current HIP device (or more than 64 devices)");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            *rc = fail(IDOLQ_ELAUNCH, std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e));
+            return nullptr;
+        }
+        addr[dev] = ptr;
+    }
+    *rc = IDOLQ_OK;
+    return addr[dev];
+}
+
+}  // namespace
+
+extern "C" size_t idolq_q8_0_gemm_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int idolq_q8_0_gemm_noalloc(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* w,
+                                       int64_t n_total, int64_t n_offset, int64_t n, const void* bias, int bias_dtype,
+                                       const void* residual, int residual_dtype, int64_t ldr, int act, int mode,
+                                       int flags, void* y, int y_dtype, int64_t ldy, void* stream) {
+    const int eff = mode == IDOLQ_MODE_AUTO ? (x_dtype == IDOLQ_F32 ? IDOLQ_MODE_EXACT : IDOLQ_MODE_DEQUANT) : mode;
+    if (eff != IDOLQ_MODE_INT8 || m <= 0 || n <= 0 || k <= 0 || k % kQ8Block)
+        // DEQUANT without a workspace runs whole tiles and EXACT needs none: nothing to take from the scratch (the
+        // GEMM's own checks handle bad shapes and empty inputs)
+        return idolq_q8_0_gemm(x, x_dtype, m, k, ldx, w, n_total, n_offset, n, bias, bias_dtype, residual,
+                               residual_dtype, ldr, act, mode, flags, y, y_dtype, ldy, nullptr, 0, stream);
+    const size_t need = idolq_q8_0_gemm_workspace(m, k, eff);
+    if (need > kNoAllocScratchBytes)
+        return fail(IDOLQ_EINVAL, "INT8 GEMM of m x k = " + std::to_string(m) + " x " + std::to_string(k) + " needs " +
+                                      std::to_string(need) + " bytes of scratch; idolq_q8_0_gemm_noalloc holds " +
+                                      std::to_string(kNoAllocScratchBytes) + " (m * k * 9 / 8 bytes at most)");
+    int rc = IDOLQ_OK;
+    void* ptr = noalloc_scratch(&rc);
+    if (!ptr) return rc;
+    return idolq_q8_0_gemm(x, x_dtype, m, k, ldx, w, n_total, n_offset, n, bias, bias_dtype, residual, residual_dtype,
+                           ldr, act, mode, flags, y, y_dtype, ldy, ptr, kNoAllocScratchBytes, stream);
 }

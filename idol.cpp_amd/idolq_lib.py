@@ -30,6 +30,9 @@ _SIGNATURES = {
     "idolq_q8_0_gemm": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _int, _vp, _int, _i64, _int,
                                _int, _int, _vp, _int, _i64, _vp, _sz, _vp]),
     "idolq_q8_0_gemm_workspace": (_sz, [_i64, _i64, _int]),
+    "idolq_q8_0_gemm_noalloc": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _int, _vp, _int, _i64,
+                                       _int, _int, _int, _vp, _int, _i64, _vp]),
+    "idolq_q8_0_gemm_noalloc_max_bytes": (_sz, []),
     "idolq_q8_0_quantize": (_int, [_vp, _i64, _i64, _i64, _vp, _vp]),
     "idolq_q8_0_tiled_bytes": (_i64, [_i64, _i64]),
     "idolq_linear_f32": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _i64, _vp, _int, _vp, _int, _i64, _vp]),

@@ -94,6 +94,18 @@ int idolq_q8_0_gemm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ld
  * IDOLQ_MODE_EXACT. */
 size_t idolq_q8_0_gemm_workspace(int64_t m, int64_t k, int mode);
 
+/* idolq_q8_0_gemm for callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc): no workspace argument, and the call allocates nothing. No counterpart in the reference.
+ * IDOLQ_MODE_INT8 takes its quantized activations and scales from a static device array of
+ * idolq_q8_0_gemm_noalloc_max_bytes() bytes (32 MiB; m * k * 9 / 8 bytes are used, larger m * k is IDOLQ_EINVAL);
+ * DEQUANT runs whole tiles (no stream-K split) and EXACT needs no scratch. Each device has its own array, shared by
+ * every call on that device: calls that overlap on one device (several streams or threads at once) race on it. */
+int idolq_q8_0_gemm_noalloc(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* w,
+                            int64_t n_total, int64_t n_offset, int64_t n, const void* bias, int bias_dtype,
+                            const void* residual, int residual_dtype, int64_t ldr, int act, int mode, int flags,
+                            void* y, int y_dtype, int64_t ldy, void* stream);
+size_t idolq_q8_0_gemm_noalloc_max_bytes(void);
+
 /* Quantizes an fp32 [n x k] matrix (row stride ldw) to Q8_0 blocks: per 32 values d = amax / 127,
  * q = round-half-away-from-zero(x * (1 / d)), d stored as fp16. The rule of ggml's quantize_row_q8_0_ref, which
  * gguf-py's quantize(..., Q8_0) restates (tools/export_full_gguf.py:332-335, tests/python/test_fused_packed.py:40). */
