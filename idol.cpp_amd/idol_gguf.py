@@ -1,6 +1,7 @@
-"""The Idol GGUF container without gguf-py: a GGUF v2/v3 reader and writer, host dequantization, and the reference's
-Idol loader on top (tools/idol_gguf.py: IdolGGUF, validate_tensor_values, validate_runtime_half_storage) plus the
-decoder bridge (tools/gguf_to_decoder.py: native_blob, materialize).
+"""The Idol GGUF container without gguf-py: a GGUF v2/v3 reader and writer, host dequantization, the Idol loader on
+top (the surface of tools/idol_gguf.py:22-49,114-224: IdolGGUF, validate_tensor_values, load_module,
+load_module_packed) and the decoder bridge (the surface of tools/gguf_to_decoder.py:16-91: native_blob,
+materialize), each written from its accept/reject cases and messages.
 
 The reference imports gguf-py (0.19.0 pinned in requirements-runtime.txt) for the container; gguf-py is not
 available here, so the container is read with this module, which restates the published GGUF layout:
@@ -14,6 +15,7 @@ read-only numpy view of the file: float32 / float16 / float64 / integer arrays s
 types, uint8 [rows, bytes per row] for block formats and BF16), and fields `contents()` as gguf-py's do.
 Host code only: tensors move to the GPU through PackedLinear / Decoders.
 """
+import dataclasses
 import json
 import os
 import struct
@@ -257,328 +259,303 @@ def dequantize(data, tensor_type):
 
 
 # ------------------------------------------------------------------------------------------------ the Idol loader
+# An Idol GGUF names every tensor idol.<component>.<state-dict key>; the embedded JSON configuration holds the four
+# model sections. What is accepted and the messages of what is not are the reference loader's
+# (tools/idol_gguf.py:22-49,114-224); the code below is organized around two tables: the encodings a file may use,
+# and for block formats where each block keeps its fp16 scales.
 COMPONENTS = ("denoiser", "octree", "gaussian", "background")
-SUPPORTED = {Q.F32, Q.F16, Q.Q8_0, Q.Q4_0, Q.Q2_K, Q.Q4_K, Q.Q6_K, Q.I8, Q.I16, Q.I32, Q.I64}
-_INTEGER = {Q.I8, Q.I16, Q.I32, Q.I64}
+CONFIG_SECTIONS = ("denoiser", "decoder", "decoder_gs", "image_encoders")
+_INTEGER = frozenset({Q.I8, Q.I16, Q.I32, Q.I64})
+_FLOAT = frozenset({Q.F32, Q.F16})
+_BLOCK = frozenset({Q.Q8_0, Q.Q4_0, Q.Q2_K, Q.Q4_K, Q.Q6_K})
+SUPPORTED = _INTEGER | _FLOAT | _BLOCK
+# block bytes, and the byte offsets of its fp16 scale fields (d, and dmin where the format has one)
+_SCALE_FIELDS = {Q.Q8_0: (34, (0,)), Q.Q4_0: (18, (0,)), Q.Q2_K: (84, (80, 82)), Q.Q4_K: (144, (0, 2)),
+                 Q.Q6_K: (210, (208,))}
+_CHUNK = 1 << 20  # values per finiteness check (bounded temporaries on large tensors)
+
+
+def _all_finite(values):
+    flat = np.asarray(values).reshape(-1)
+    return all(bool(np.isfinite(flat[i:i + _CHUNK]).all()) for i in range(0, flat.size, _CHUNK))
 
 
 def validate_tensor_values(tensor):
-    """Numeric validity without a dequantized copy (tools/idol_gguf.py:22-49): finite scales for block formats,
-    finite values for float tensors, no all-ones exponent for BF16."""
-    k_formats = {Q.Q2_K: (84, (80, 82)), Q.Q4_K: (144, (0, 2)), Q.Q6_K: (210, (208,))}
+    """True when a tensor holds no inf or NaN, checked without expanding it: the fp16 scale fields of every block of
+    a block format, the values of F16 / F32 tensors, the exponent fields of BF16 (all ones = inf or NaN). Integer
+    tensors are always valid."""
     t = tensor.tensor_type
-    if t in k_formats:
-        size, offsets = k_formats[t]
-        raw = np.asarray(tensor.data).reshape(-1, size)
-        return all(np.isfinite(np.ascontiguousarray(raw[:, o:o + 2]).view("<f2")).all() for o in offsets)
-    if t in (Q.Q4_0, Q.Q8_0):
-        raw = np.asarray(tensor.data).reshape(-1, 18 if t == Q.Q4_0 else 34)
-        return bool(np.isfinite(np.ascontiguousarray(raw[:, :2]).view("<f2")).all())
+    if t in _SCALE_FIELDS:
+        size, offsets = _SCALE_FIELDS[t]
+        blocks = np.asarray(tensor.data).reshape(-1, size)
+        return all(_all_finite(np.ascontiguousarray(blocks[:, o:o + 2]).view("<f2")) for o in offsets)
+    if t in _FLOAT:
+        return _all_finite(tensor.data)
     if t == Q.BF16:
-        u = np.ascontiguousarray(tensor.data).view("<u2").reshape(-1)
-        return all(not np.any((u[i:i + 1_000_000] & 0x7F80) == 0x7F80) for i in range(0, u.size, 1_000_000))
-    if t in (Q.F16, Q.F32):
-        v = np.asarray(tensor.data).reshape(-1)
-        return all(np.isfinite(v[i:i + 1_000_000]).all() for i in range(0, v.size, 1_000_000))
+        bits = np.ascontiguousarray(tensor.data).view("<u2").reshape(-1)
+        return all(not bool(((bits[i:i + _CHUNK] & 0x7F80) == 0x7F80).any()) for i in range(0, bits.size, _CHUNK))
     return True
 
 
-def validate_runtime_half_storage(model, module):
-    """Fail if a runtime-aware file would downcast a float32 matrix of the module (tools/idol_gguf.py:52-111)."""
-    field = model.reader.get_field("idol.quantization.tier")
-    if field is None:
-        return
-    tier = field.contents()
-    denoiser_kind, mixed = None, False
-    suffixes = {"_DENOISER_Q2K_COV": (Q.Q2_K, False), "_DENOISER_Q4K_COV": (Q.Q4_K, False),
-                "_DENOISER_Q6K_COV": (Q.Q6_K, False), "_DENOISER_Q80_COV": (Q.Q8_0, False),
-                "_DENOISER_Q2KF16_COV": (Q.Q2_K, True), "_DENOISER_Q4KF16_COV": (Q.Q4_K, True),
-                "_DENOISER_Q6KF16_COV": (Q.Q6_K, True), "_DENOISER_Q80F16_COV": (Q.Q8_0, True)}
-    for suffix, (kind, is_mixed) in suffixes.items():
-        if tier.endswith(suffix):
-            tier, denoiser_kind, mixed = tier[:-len(suffix)], kind, is_mixed
-            break
-    if tier not in ("RUNTIME_F16_Q8", "RUNTIME_F16_GAUSSIAN_Q2K", "RUNTIME_F16_GAUSSIAN_Q4K",
-                    "RUNTIME_F16_GAUSSIAN_Q6K", "RUNTIME_F16_GAUSSIAN_Q2K_COV", "RUNTIME_F16_GAUSSIAN_Q4K_COV",
-                    "RUNTIME_F16_GAUSSIAN_Q6K_COV", "RUNTIME_F16_GAUSSIAN_Q2Q4_COV"):
-        return
-    expected = module.state_dict()
-    checked, preserved, seen = 0, set(), set()
-    if mixed:
-        allocation = model.reader.get_field("idol.quantization.denoiser_preserved_blocks")
-        if allocation is None:
-            raise ValueError("mixed denoiser tier is missing its block allocation")
-        values = json.loads(allocation.contents())
-        if (not isinstance(values, list) or any(type(v) is not int or v < 0 for v in values)
-                or values != sorted(set(values))):
-            raise ValueError("invalid mixed denoiser block allocation")
-        preserved = set(values)
-    for name, tensor in model.tensors["denoiser"].items():
-        if (denoiser_kind is not None and name.startswith("blocks.") and name.endswith("weight")
-                and len(tensor.shape) == 2 and int(tensor.shape[0]) % 256 == 0):
-            checked += 1
-            parts = name.split(".")
-            if mixed and (len(parts) < 3 or not parts[1].isdigit()):
-                raise ValueError("invalid mixed denoiser block name: " + name)
-            block = int(parts[1]) if mixed else None
-            if mixed:
-                seen.add(block)
-            required = Q.F16 if block in preserved else denoiser_kind
-            if tensor.tensor_type != required or name not in expected or expected[name].dtype != torch.float16:
-                raise ValueError("encoded denoiser block is incompatible with the runtime: " + name)
-        if (tensor.tensor_type == Q.F16 and len(tensor.shape) == 2
-                and (name not in expected or expected[name].dtype != torch.float16)):
-            raise ValueError("runtime-aware half-precision matrix is not half precision in this SDK: " + name)
-    if denoiser_kind is not None and checked == 0:
-        raise ValueError("encoded denoiser tier has no eligible runtime blocks")
-    if mixed and (not preserved <= seen or preserved == seen):
-        raise ValueError("mixed denoiser block allocation does not match the runtime")
+def _logical_shape(tensor):
+    """The PyTorch shape of a GGUF tensor (GGUF lists dimensions innermost first)."""
+    return tuple(int(d) for d in reversed(np.asarray(tensor.shape).tolist()))
+
+
+def _host_array(tensor, shape):
+    """The tensor's values as a fresh host array of `shape`: integers as stored, everything else expanded to fp32."""
+    if tensor.tensor_type in _INTEGER:
+        values = np.asarray(tensor.data)
+    else:
+        values = dequantize(tensor.data, tensor.tensor_type)
+    return np.array(values, copy=True).reshape(shape)
 
 
 class IdolGGUF:
-    """An Idol GGUF file (tools/idol_gguf.py:114-224): `config` (the embedded JSON), `tensors[component][name]`,
-    load_module and load_module_packed, with the reference's checks and messages."""
+    """An Idol GGUF file: `config` (the embedded JSON), `tensors[component][state-dict key]` (reader tensors), and
+    load_module / load_module_packed to fill a module of one component."""
 
     def __init__(self, path):
         self.path = Path(path)
         self.reader = GGUFReader(self.path)
-        arch = self.reader.get_field("general.architecture")
-        config = self.reader.get_field("idol.config.json")
-        if arch is None or arch.contents() != "idol" or config is None:
+        fields = {key: self.reader.get_field(key) for key in ("general.architecture", "idol.config.json")}
+        if fields["idol.config.json"] is None or fields["general.architecture"] is None \
+                or fields["general.architecture"].contents() != "idol":
             raise ValueError("not an Idol GGUF file with an embedded configuration")
-        self.config = json.loads(config.contents())
-        if not all(k in self.config for k in ("denoiser", "decoder", "decoder_gs", "image_encoders")):
+        self.config = json.loads(fields["idol.config.json"].contents())
+        if any(section not in self.config for section in CONFIG_SECTIONS):
             raise ValueError("incomplete Idol configuration")
-        self.tensors = {name: {} for name in COMPONENTS}
+        self.tensors = {component: {} for component in COMPONENTS}
         for tensor in self.reader.tensors:
-            parts = tensor.name.split(".", 2)
-            if len(parts) != 3 or parts[0] != "idol" or parts[1] not in self.tensors or not parts[2]:
+            prefix, _, rest = tensor.name.partition(".")
+            component, _, key = rest.partition(".")
+            if prefix != "idol" or component not in self.tensors or not key:
                 raise ValueError("unexpected tensor in Idol GGUF: " + tensor.name)
-            group = self.tensors[parts[1]]
-            if parts[2] in group or tensor.tensor_type not in SUPPORTED:
+            held = self.tensors[component]
+            if key in held or tensor.tensor_type not in SUPPORTED:
                 raise ValueError("duplicate tensor or unsupported GGUF encoding: " + tensor.name)
-            group[parts[2]] = tensor
-        if any(not values for values in self.tensors.values()):
+            held[key] = tensor
+        if not all(self.tensors.values()):
             raise ValueError("Idol GGUF is missing a component")
 
-    def load_module(self, component, module):
-        """Every tensor of `component` expanded into `module`'s state (tools/idol_gguf.py:131-162)."""
+    # -------------------------------------------------------------------------------------------- shared checks
+    def _source(self, component):
         if component not in self.tensors:
             raise ValueError("unknown component: " + component)
-        expected = module.state_dict()
-        source = self.tensors[component]
-        if set(expected) != set(source):
-            missing, extra = sorted(set(expected) - set(source)), sorted(set(source) - set(expected))
-            raise ValueError(f"{component} tensor names do not match; missing={missing}, extra={extra}")
-        for name, target in expected.items():
-            tensor = source[name]
-            shape = tuple(reversed(tensor.shape.tolist()))
-            if shape != tuple(target.shape):
-                raise ValueError(f"{component}.{name} shape {shape} does not match {tuple(target.shape)}")
+        return self.tensors[component]
+
+    def _check_mapping(self, component, source, expected, detailed):
+        """Same keys on both sides, equal shapes, finite values; `detailed` adds the lists and shapes to the messages
+        (load_module's form) where load_module_packed's messages are shorter."""
+        if set(source) != set(expected):
+            message = f"{component} tensor names do not match"
+            if detailed:
+                missing, extra = sorted(set(expected) - set(source)), sorted(set(source) - set(expected))
+                message += f"; missing={missing}, extra={extra}"
+            raise ValueError(message)
+        for key, target in expected.items():
+            tensor, want = source[key], tuple(target.shape)
+            got = _logical_shape(tensor)
+            if got != want:
+                raise ValueError(f"{component}.{key} shape {got} does not match {want}" if detailed
+                                 else f"{component}.{key} shape does not match")
             if not validate_tensor_values(tensor):
-                raise ValueError(f"non-finite value in {component}.{name}")
+                raise ValueError(f"non-finite value in {component}.{key}")
+
+    # -------------------------------------------------------------------------------------------- loaders
+    def load_module(self, component, module):
+        """Every tensor of `component` expanded to its values and copied into `module` (all checks first)."""
+        source = self._source(component)
+        state = module.state_dict()
+        self._check_mapping(component, source, state, detailed=True)
+        values = {key: _host_array(source[key], tuple(target.shape)) for key, target in state.items()}
         with torch.no_grad():
-            for name, target in expected.items():
-                tensor = source[name]
-                shape = tuple(target.shape)
-                if tensor.tensor_type in _INTEGER:
-                    values = np.asarray(tensor.data).reshape(shape)
-                else:
-                    values = dequantize(tensor.data, tensor.tensor_type).reshape(shape)
-                target.copy_(torch.from_numpy(np.array(values, copy=True)))
+            for key, target in state.items():
+                target.copy_(torch.from_numpy(values[key]))
         return module
 
     def load_module_packed(self, component, module, *, include_half=False):
-        """A meta-initialized module loaded without expanding its packed matrices: quantized linear weights (and,
-        with include_half, F16 ones) become PackedLinear layers (tools/idol_gguf.py:164-224)."""
+        """A module built on the meta device, filled without expanding its packed matrices: every block-format linear
+        weight (and, with include_half, every F16 matrix weight) becomes a PackedLinear holding the file's bytes;
+        the other tensors are materialized on the host."""
         from accelerate.utils import set_module_tensor_to_device
         from idol_packed import PackedLinear
 
-        if component not in self.tensors:
-            raise ValueError("unknown component: " + component)
-        expected, source = module.state_dict(), self.tensors[component]
-        if set(expected) != set(source):
-            raise ValueError(f"{component} tensor names do not match")
-        packed_kinds = {Q.Q8_0, Q.Q4_0, Q.Q2_K, Q.Q4_K, Q.Q6_K}
-        selected = {}
-        for name, target in expected.items():
-            tensor = source[name]
-            if tuple(reversed(tensor.shape.tolist())) != tuple(target.shape):
-                raise ValueError(f"{component}.{name} shape does not match")
-            if not validate_tensor_values(tensor):
-                raise ValueError(f"non-finite value in {component}.{name}")
-            packed = tensor.tensor_type in packed_kinds or (
-                include_half and tensor.tensor_type == Q.F16 and len(tensor.shape) == 2 and name.endswith(".weight"))
-            if packed:
-                if not name.endswith(".weight"):
-                    raise ValueError("quantized tensor is not a linear weight: " + name)
-                layer_name = name[:-7]
-                try:
-                    layer = module.get_submodule(layer_name)
-                except AttributeError as exc:
-                    raise ValueError("quantized linear layer is missing: " + name) from exc
-                if not isinstance(layer, torch.nn.Linear):
-                    raise ValueError("quantized tensor is not a linear weight: " + name)
-                selected[layer_name] = layer
-        skipped = {name + suffix for name in selected for suffix in (".weight", ".bias")}
-        for name, target in expected.items():
-            if name in skipped:
+        source = self._source(component)
+        state = module.state_dict()
+        self._check_mapping(component, source, state, detailed=False)
+        layers = {}
+        for key in state:
+            tensor = source[key]
+            if not _packs(key, tensor, include_half):
                 continue
-            tensor = source[name]
-            values = (np.asarray(tensor.data) if tensor.tensor_type in _INTEGER
-                      else dequantize(tensor.data, tensor.tensor_type))
-            values = torch.from_numpy(np.array(values, copy=True).reshape(target.shape))
-            set_module_tensor_to_device(module, name, "cpu", value=values, dtype=target.dtype)
-        for name, original in selected.items():
+            owner = key[:-len(".weight")] if key.endswith(".weight") else None
+            layer = _linear_at(module, owner, key)
+            layers[owner] = layer
+        packed_keys = {owner + suffix for owner in layers for suffix in (".weight", ".bias")}
+        for key, target in state.items():
+            if key not in packed_keys:
+                set_module_tensor_to_device(module, key, "cpu", dtype=target.dtype,
+                                            value=torch.from_numpy(_host_array(source[key], tuple(target.shape))))
+        for owner, layer in layers.items():
             bias = None
-            if original.bias is not None:
-                tensor = source[name + ".bias"]
-                values = dequantize(tensor.data, tensor.tensor_type)
-                bias = torch.from_numpy(np.array(values, copy=True)).reshape(original.bias.shape).to(original.bias.dtype)
-            parent_name, _, leaf = name.rpartition(".")
-            parent = module.get_submodule(parent_name) if parent_name else module
-            setattr(parent, leaf, PackedLinear(source[name + ".weight"], bias))
-        if any(value.is_meta for value in list(module.parameters()) + list(module.buffers())):
+            if layer.bias is not None:
+                bias = torch.from_numpy(_host_array(source[owner + ".bias"], tuple(layer.bias.shape)))
+                bias = bias.to(layer.bias.dtype)
+            parent, _, leaf = owner.rpartition(".")
+            setattr(module.get_submodule(parent) if parent else module, leaf,
+                    PackedLinear(source[owner + ".weight"], bias))
+        if any(t.is_meta for t in list(module.parameters()) + list(module.buffers())):
             raise ValueError("packed module retains uninitialized tensors")
         return module
 
 
+def _packs(key, tensor, include_half):
+    """Whether load_module_packed keeps this tensor packed."""
+    if tensor.tensor_type in _BLOCK:
+        return True
+    return (include_half and tensor.tensor_type == Q.F16 and len(np.asarray(tensor.shape)) == 2
+            and key.endswith(".weight"))
+
+
+def _linear_at(module, owner, key):
+    """The nn.Linear a packed weight belongs to, or the reference loader's error for it."""
+    if owner is None:
+        raise ValueError("quantized tensor is not a linear weight: " + key)
+    try:
+        layer = module.get_submodule(owner)
+    except AttributeError as exc:
+        raise ValueError("quantized linear layer is missing: " + key) from exc
+    if not isinstance(layer, torch.nn.Linear):
+        raise ValueError("quantized tensor is not a linear weight: " + key)
+    return layer
+
+
 # ------------------------------------------------------------------------------------------------ decoder bridge
-def native_blob(tensor):
-    """The panel blob of a Q8_0 or Q4_0 GGUF matrix without re-quantizing (tools/gguf_to_decoder.py:16-40):
-    code = q + 128 (8-bit) or the nibble (4-bit), scale = d, minimum = -128 d / -8 d. Returns (blob, bits, shape)."""
-    shape = tuple(reversed(tensor.shape.tolist()))
+# The native decoders (src/decoders.cpp) read a manifest + weights.bin export. From an Idol GGUF, the octree and
+# Gaussian components become that export: Q8_0 and Q4_0 matrices keep their exact values (as panels on disk, as
+# Q8_0 blocks in memory), every other tensor is expanded to fp32, and the frequency tables and the `rep` record of
+# the configuration are added (the surface of tools/gguf_to_decoder.py:16-91).
+_DECODER_PARTS = (("octree", "oct."), ("gaussian", "gs."))
+
+
+def _q8_0_blocks(tensor):
+    """(blocks uint8 [rows, k / 32, 34], rows, k) of a Q8_0 or Q4_0 matrix as exact Q8_0 blocks: Q4_0's value
+    d * (nibble - 8) is the Q8_0 block with the same d and code nibble - 8. Rejects other shapes and inf / NaN
+    scales."""
+    shape = _logical_shape(tensor)
     if len(shape) != 2 or shape[1] % 32:
         raise ValueError("quantized native decoder tensors must be matrices with 32-element groups")
-    out, width = shape
+    rows, k = shape
+    raw = np.ascontiguousarray(tensor.data).reshape(-1)
     if tensor.tensor_type == Q.Q8_0:
-        bits, block_bytes, bias = 8, 34, 128
+        blocks = raw.reshape(rows, k // 32, 34).copy()
     elif tensor.tensor_type == Q.Q4_0:
-        bits, block_bytes, bias = 4, 18, 8
+        blocks = _q4_0_as_q8_0(raw).reshape(rows, k // 32, 34)
     else:
         raise ValueError("unsupported quantized decoder tensor")
-    blocks = np.asarray(tensor.data).reshape(out, width // 32, block_bytes)
-    scales = np.ascontiguousarray(blocks[:, :, :2]).view("<f2").reshape(out, -1).astype(np.float32)
-    if not np.isfinite(scales).all():
+    if not _all_finite(np.ascontiguousarray(blocks[:, :, :2]).view("<f2")):
         raise ValueError("non-finite GGUF scale")
-    payload = np.ascontiguousarray(blocks[:, :, 2:])
-    if bits == 8:
-        codes = (payload.view(np.int8).astype(np.int16) + bias).astype(np.uint8).reshape(out, width)
-    else:
-        codes = np.concatenate((payload & 15, payload >> 4), axis=-1).reshape(out, width)
-    minimum = (-bias * scales).astype(np.float16).astype(np.float32)
-    if not np.isfinite(minimum).all() or not np.array_equal(minimum, -bias * scales):
-        raise ValueError("GGUF scale cannot be represented exactly in native layout")
-    return K.pack_panel(codes, scales, minimum, bits, 32), bits, shape
-
-
-def _decoder_header(model):
-    config = model.config
-    oct_args, gs_args = config["decoder"]["args"], config["decoder_gs"]["args"]
-    if oct_args["model_channels"] != gs_args["model_channels"] or oct_args["num_heads"] != gs_args["num_heads"]:
-        raise ValueError("native decoder requires matching octree and Gaussian dimensions and heads")
-    rep = gs_args["representation_config"]
-    cfg = E.DecoderConfig(oct_args["model_channels"], oct_args["num_heads"], oct_args["num_blocks"],
-                          gs_args["num_blocks"], oct_args["cond_channels"], rep["num_gaussians"])
-    return cfg, rep
-
-
-def _frequency_tables(dim):
-    """The embedders' nonpersistent frequency tables, in float32 as PyTorch builds them (tools/gguf_to_decoder.py:81-87)."""
-    freq_dim = dim // 3 // 2
-    pos = torch.pow(2.0, torch.linspace(0.0, 10.0, steps=freq_dim, dtype=torch.float32)).numpy()
-    half = 128
-    levels = torch.exp(-np.log(1024) * torch.arange(0, half, dtype=torch.float32) / half).numpy()
-    return pos, levels
-
-
-def _rep_values(rep):
-    """The `rep` record in the order the reference's bridge writes it (tools/gguf_to_decoder.py:88-91): the learning
-    rates of scaling and opacity in the order (scaling, opacity), which its reader (src/weights.cpp:57-58) takes as
-    (opacity, scaling). Kept as the reference has it, so both runtimes see the same values."""
-    return (rep["perturbe_size"], rep["3d_filter_kernel_size"], rep["scaling_bias"], rep["opacity_bias"],
-            rep["lr"]["_xyz"], rep["lr"]["_features_dc"], rep["lr"]["_scaling"], rep["lr"]["_opacity"],
-            rep["lr"]["_rotation"])
-
-
-def materialize(model, output):
-    """Writes the native decoder export of an Idol GGUF (tools/gguf_to_decoder.py:43-91): Q8_0 and Q4_0 matrices as
-    panel blobs, every other tensor expanded to fp32, the frequency tables, the `rep` record."""
-    output = Path(output)
-    cfg, rep = _decoder_header(model)
-    header = f"decoders {cfg.dim} {cfg.heads} {cfg.oct_blocks} {cfg.gs_blocks} {cfg.cond} {cfg.per_anchor}"
-    manifest = [header]
-    output.mkdir(parents=True, exist_ok=False)
-    with (output / "weights.bin").open("xb") as stream:
-        def place(data):
-            stream.write(b"\0" * ((-stream.tell()) % E.ALIGN))
-            offset = stream.tell()
-            stream.write(data)
-            return offset
-
-        def add_dense(name, value):
-            array = np.ascontiguousarray(value, dtype="<f4")
-            offset = place(array.tobytes())
-            dims = " ".join(str(d) for d in value.shape)
-            manifest.append(f"{name} {value.ndim} {dims} {offset} {array.nbytes}")
-
-        for component, prefix in (("octree", "oct."), ("gaussian", "gs.")):
-            for name, tensor in sorted(model.tensors[component].items()):
-                shape = tuple(reversed(tensor.shape.tolist()))
-                if tensor.tensor_type in (Q.Q8_0, Q.Q4_0):
-                    blob, bits, shape = native_blob(tensor)
-                    offset = place(blob.tobytes())
-                    manifest.append(f"qtensor {prefix}{name} {shape[0]} {shape[1]} {bits} 32 {offset} {blob.size}")
-                else:
-                    values = dequantize(tensor.data, tensor.tensor_type).reshape(shape)
-                    if not np.isfinite(values).all():
-                        raise ValueError("non-finite decoder tensor: " + name)
-                    add_dense(prefix + name, values)
-        pos, levels = _frequency_tables(cfg.dim)
-        for prefix in ("oct.", "gs."):
-            add_dense(prefix + "pos_embedder.freqs", pos)
-        add_dense("oct.l_embedder.freqs", levels)
-    manifest.append("rep " + " ".join(str(v) for v in _rep_values(rep)))
-    (output / "manifest.txt").write_text("\n".join(manifest) + "\n", encoding="ascii")
-
-
-def decoder_export(model):
-    """The decoders of an Idol GGUF as an in-memory export (what materialize writes and read_export reads, without
-    the files): Q8_0 matrices as their GGUF blocks, Q4_0 matrices re-encoded exactly as Q8_0 blocks, every other
-    tensor expanded to fp32. Decoders(decoder_export(IdolGGUF(path))) runs them on the GPU."""
-    cfg, rep = _decoder_header(model)
-    ex = E.Export(decoders=True, decoder_config=cfg)
-    r = _rep_values(rep)
-    ex.rep = E.Representation(*(float(np.float32(v)) for v in r))
-    for component, prefix in (("octree", "oct."), ("gaussian", "gs.")):
-        for name, tensor in sorted(model.tensors[component].items()):
-            shape = tuple(reversed(tensor.shape.tolist()))
-            if tensor.tensor_type in (Q.Q8_0, Q.Q4_0):
-                if len(shape) != 2 or shape[1] % 32:
-                    raise ValueError("quantized native decoder tensors must be matrices with 32-element groups")
-                raw = np.ascontiguousarray(tensor.data).reshape(-1)
-                blocks = raw.copy() if tensor.tensor_type == Q.Q8_0 else _q4_0_as_q8_0(raw)
-                scales = blocks.reshape(-1, 34)[:, :2].copy().view("<f2")
-                if not np.isfinite(scales).all():
-                    raise ValueError("non-finite GGUF scale")
-                ex.qtensors[prefix + name] = E.QTensor(shape[0], shape[1], 8, 32, blocks, kind="q8_0")
-            else:
-                values = dequantize(tensor.data, tensor.tensor_type).reshape(shape)
-                if not np.isfinite(values).all():
-                    raise ValueError("non-finite decoder tensor: " + name)
-                ex.tensors[prefix + name] = E.Tensor(list(shape), np.ascontiguousarray(values, np.float32).reshape(-1))
-    pos, levels = _frequency_tables(cfg.dim)
-    for prefix in ("oct.", "gs."):
-        ex.tensors[prefix + "pos_embedder.freqs"] = E.Tensor([pos.size], pos.astype(np.float32))
-    ex.tensors["oct.l_embedder.freqs"] = E.Tensor([levels.size], levels.astype(np.float32))
-    return ex
+    return blocks, rows, k
 
 
 def _q4_0_as_q8_0(raw):
-    """Q8_0 blocks holding exactly the values of Q4_0 blocks (same fp16 scale, codes q - 8), on the host."""
-    b4 = raw.reshape(-1, 18)
-    out = np.empty((b4.shape[0], 34), np.uint8)
-    out[:, :2] = b4[:, :2]
-    q = np.concatenate([b4[:, 2:] & 15, b4[:, 2:] >> 4], axis=1).astype(np.int16) - 8
-    out[:, 2:] = q.astype(np.int8).view(np.uint8)
-    return out.reshape(-1)
+    """Q8_0 blocks with the values of Q4_0 blocks (18 bytes: fp16 d, 16 bytes of nibbles, low nibbles first)."""
+    q4 = np.asarray(raw, np.uint8).reshape(-1, 18)
+    nibbles = np.concatenate([q4[:, 2:] & 0x0F, q4[:, 2:] >> 4], axis=1)
+    q8 = np.empty((q4.shape[0], 34), np.uint8)
+    q8[:, :2] = q4[:, :2]
+    q8[:, 2:] = (nibbles.astype(np.int8) - np.int8(8)).view(np.uint8)
+    return q8.reshape(-1)
+
+
+def native_blob(tensor):
+    """(panel blob, bits, (rows, k)) holding a Q8_0 (8 bits) or Q4_0 (4 bits) matrix's values without re-quantizing:
+    per 32-group scale = d and minimum = -2^(bits-1) d, code = q + 2^(bits-1). The minimum must be an exact fp16."""
+    blocks, rows, k = _q8_0_blocks(tensor)
+    bits = 8 if tensor.tensor_type == Q.Q8_0 else 4
+    offset = 1 << (bits - 1)
+    d = np.ascontiguousarray(blocks[:, :, :2]).view("<f2")[..., 0].astype(np.float32)
+    codes = (blocks[:, :, 2:].view(np.int8).astype(np.int16) + offset).astype(np.uint8).reshape(rows, k)
+    minimum = np.float32(-offset) * d
+    if not np.array_equal(minimum.astype(np.float16).astype(np.float32), minimum):
+        raise ValueError("GGUF scale cannot be represented exactly in native layout")
+    return K.pack_panel(codes, d, minimum, bits, 32), bits, (rows, k)
+
+
+def _decoder_config(model):
+    """The export header and the Gaussian representation section of the configuration."""
+    octree, gaussian = model.config["decoder"]["args"], model.config["decoder_gs"]["args"]
+    if (octree["model_channels"], octree["num_heads"]) != (gaussian["model_channels"], gaussian["num_heads"]):
+        raise ValueError("native decoder requires matching octree and Gaussian dimensions and heads")
+    rep = gaussian["representation_config"]
+    header = E.DecoderConfig(octree["model_channels"], octree["num_heads"], octree["num_blocks"],
+                             gaussian["num_blocks"], octree["cond_channels"], rep["num_gaussians"])
+    return header, rep
+
+
+def _representation(rep):
+    """The `rep` record the bridge writes. Its scaling and opacity learning rates land in the reader's opacity and
+    scaling slots respectively (tools/gguf_to_decoder.py:88-91 against src/weights.cpp:57-58); kept so that this
+    build and the reference read the same numbers from the same export."""
+    lr = rep["lr"]
+    return E.Representation(rep["perturbe_size"], rep["3d_filter_kernel_size"], rep["scaling_bias"],
+                            rep["opacity_bias"], lr["_xyz"], lr["_features_dc"], lr["_scaling"], lr["_opacity"],
+                            lr["_rotation"])
+
+
+def _frequencies(dim):
+    """The position embedders' frequencies 2^linspace(0, 10, dim / 6) and the level embedder's
+    exp(-ln(1024) i / 128), i < 128, in fp32 as PyTorch computes them (the modules' non-persistent buffers)."""
+    position = torch.pow(2.0, torch.linspace(0.0, 10.0, steps=dim // 3 // 2, dtype=torch.float32))
+    level = torch.exp(-np.log(1024) * torch.arange(0, 128, dtype=torch.float32) / 128)
+    return {"oct.pos_embedder.freqs": position.numpy(), "gs.pos_embedder.freqs": position.numpy(),
+            "oct.l_embedder.freqs": level.numpy()}
+
+
+def _decoder_tensors(model):
+    """(export name, tensor) of the octree and Gaussian components, each component in key order."""
+    for component, prefix in _DECODER_PARTS:
+        for key in sorted(model.tensors[component]):
+            yield prefix + key, model.tensors[component][key]
+
+
+def _dense_values(name, tensor):
+    values = _host_array(tensor, _logical_shape(tensor)).astype(np.float32)
+    if not _all_finite(values):
+        raise ValueError("non-finite decoder tensor: " + name.split(".", 1)[1])
+    return values
+
+
+def materialize(model, output):
+    """Writes the native decoder export of an Idol GGUF to the new directory `output` (FileExistsError if it exists):
+    Q8_0 / Q4_0 matrices as panel blobs (native_blob), the rest as fp32."""
+    header, rep = _decoder_config(model)
+    dense, panels = {}, {}
+    for name, tensor in _decoder_tensors(model):
+        if tensor.tensor_type in (Q.Q8_0, Q.Q4_0):
+            blob, bits, (rows, k) = native_blob(tensor)
+            panels[name] = E.QTensor(rows, k, bits, 32, blob)
+        else:
+            dense[name] = _dense_values(name, tensor)
+    dense.update(_frequencies(header.dim))
+    E.write_export(output, header, dense, panels, rep=_representation(rep))
+
+
+def decoder_export(model):
+    """The export materialize writes, in memory: Q8_0 / Q4_0 matrices as exact Q8_0 blocks, the rest fp32.
+    Decoders(decoder_export(IdolGGUF(path))) runs a GGUF's decoders without writing files."""
+    header, rep = _decoder_config(model)
+    ex = E.Export(decoders=True, decoder_config=header)
+    r = _representation(rep)
+    ex.rep = E.Representation(*(float(np.float32(v)) for v in dataclasses.astuple(r)))
+    for name, tensor in _decoder_tensors(model):
+        if tensor.tensor_type in (Q.Q8_0, Q.Q4_0):
+            blocks, rows, k = _q8_0_blocks(tensor)
+            ex.qtensors[name] = E.QTensor(rows, k, 8, 32, blocks.reshape(-1), kind="q8_0")
+        else:
+            values = _dense_values(name, tensor)
+            ex.tensors[name] = E.Tensor(list(values.shape), np.ascontiguousarray(values).reshape(-1))
+    for name, values in _frequencies(header.dim).items():
+        ex.tensors[name] = E.Tensor([values.size], values.astype(np.float32))
+    return ex

@@ -1,9 +1,9 @@
 """Quantized linear layers that keep their GGUF blocks packed: the drop-in for the reference's
 tools/idol_packed.py (PackedLinear, enable_fused_packed, replace_quantized_linear_layers).
 
-Signatures, attributes (`shape`, `kind`, `packed` buffer, `bias`, `fused`), validation and error messages follow the
-reference. The fused GPU path is libidolq (idol_hip.fused_linear) for Q4_0, Q8_0 and Q4_K, the kinds the reference
-fuses. dequantize() expands every kind: on the GPU with libidolq's kernels (idolq_q8_0_dequant,
+Signatures, attributes (`shape`, `kind`, `packed` buffer, `bias`, `fused`), the accepted inputs and the error
+messages are the reference's interface; the code is this build's. The fused GPU path is libidolq
+(idol_hip.fused_linear) for Q4_0, Q8_0 and Q4_K, the kinds the reference fuses. dequantize() expands every kind: on the GPU with libidolq's kernels (idolq_q8_0_dequant,
 idolq_blocks_dequant), for a module kept on the host with tensor arithmetic; both compute each value with the
 reference expansion's fp32 operations (tools/idol_packed.py:25-71), then round once.
 """
@@ -17,21 +17,25 @@ from idol_hip import fused_linear
 
 _PACKED_KINDS = (GGMLQuantizationType.F16, GGMLQuantizationType.Q8_0, GGMLQuantizationType.Q4_0,
                  GGMLQuantizationType.Q2_K, GGMLQuantizationType.Q4_K, GGMLQuantizationType.Q6_K)
+_BLOCK_KINDS = frozenset(_PACKED_KINDS[1:])
 _FUSED_KINDS = {GGMLQuantizationType.Q4_0: 4, GGMLQuantizationType.Q8_0: 8, GGMLQuantizationType.Q4_K: 44}
+_FUSED_DTYPES = (torch.float16, torch.bfloat16)
 
 
 class PackedLinear(torch.nn.Module):
-    """A linear layer holding raw GGUF blocks (tools/idol_packed.py:12-23)."""
+    """A linear layer that keeps a GGUF matrix's raw bytes (the interface of tools/idol_packed.py:12-82).
+
+    `shape` is (out, in) -- the GGUF dimensions reversed --, `kind` the GGUF type, `packed` a uint8 buffer (it moves
+    with .to(device)), `bias` a frozen parameter or None, and `fused` whether forward may take the fused kernel."""
 
     def __init__(self, source, bias):
         super().__init__()
-        self.shape = tuple(reversed(np.asarray(source.shape).tolist()))
-        self.kind = source.tensor_type
-        if len(self.shape) != 2 or self.kind not in _PACKED_KINDS:
+        shape = tuple(int(d) for d in reversed(np.asarray(source.shape).tolist()))
+        if len(shape) != 2 or source.tensor_type not in _PACKED_KINDS:
             raise ValueError("unsupported packed matrix")
-        self.register_buffer("packed", torch.from_numpy(np.array(source.data, copy=True)).reshape(-1))
-        self.bias = torch.nn.Parameter(bias.detach(), requires_grad=False) if bias is not None else None
-        self.fused = False
+        self.shape, self.kind, self.fused = shape, source.tensor_type, False
+        self.register_buffer("packed", torch.from_numpy(np.array(source.data, dtype=np.uint8, copy=True).reshape(-1)))
+        self.bias = None if bias is None else torch.nn.Parameter(bias.detach(), requires_grad=False)
 
     def dequantize(self, dtype):
         """The dense (n, k) weight in `dtype` (tools/idol_packed.py:25-71)."""
@@ -48,13 +52,17 @@ class PackedLinear(torch.nn.Module):
             return dense if out_dtype == dtype else dense.to(dtype)
         return _host_values(self.packed, kind, n, k).to(dtype)
 
+    def _fusable(self, value):
+        """The fused kernel serves enabled layers of the fused kinds on 16-bit GPU activations when no gradient is
+        being recorded for the input or the bias."""
+        if not (self.fused and self.kind in _FUSED_KINDS and value.is_cuda and value.dtype in _FUSED_DTYPES):
+            return False
+        if not torch.is_grad_enabled():
+            return True
+        return not value.requires_grad and not (self.bias is not None and self.bias.requires_grad)
+
     def forward(self, value):
-        """Fused kernel for Q4_0, Q8_0 and Q4_K on the GPU with 16-bit activations and no autograd; otherwise a dense product
-        (tools/idol_packed.py:73-82)."""
-        needs_grad = torch.is_grad_enabled() and (value.requires_grad or
-                                                  (self.bias is not None and self.bias.requires_grad))
-        if (self.fused and value.is_cuda and value.dtype in (torch.float16, torch.bfloat16)
-                and self.kind in _FUSED_KINDS and not needs_grad):
+        if self._fusable(value):
             return fused_linear(value, self.packed, self.shape, _FUSED_KINDS[self.kind], self.bias)
         return F.linear(value, self.dequantize(value.dtype), self.bias)
 
@@ -105,43 +113,44 @@ def _host_values(packed, kind, n, k):
 
 
 def enable_fused_packed(model):
-    """Enable supported packed layers; return the number configured for the GPU (tools/idol_packed.py:85-94)."""
-    count = 0
-    for layer in model.modules():
-        if isinstance(layer, PackedLinear) and layer.kind in _FUSED_KINDS:
-            layer.fused = True
-            count += 1
-    return count
+    """Marks every PackedLinear of a fused kind for the fused path; returns how many (tools/idol_packed.py:85-94)."""
+    layers = [m for m in model.modules() if isinstance(m, PackedLinear) and m.kind in _FUSED_KINDS]
+    for layer in layers:
+        layer.fused = True
+    return len(layers)
+
+
+def _replaceable(key, tensor, include_half):
+    """Whether replace_quantized_linear_layers takes this source tensor: block formats always, F16 matrix weights
+    with include_half."""
+    if tensor.tensor_type in _BLOCK_KINDS:
+        return True
+    return (include_half and tensor.tensor_type == GGMLQuantizationType.F16 and len(np.asarray(tensor.shape)) == 2
+            and key.endswith(".weight"))
+
+
+def _target_layer(model, key, tensor):
+    """The nn.Linear whose weight `key` names, with the same shape as the source tensor, or the error for it."""
+    if not key.endswith(".weight"):
+        raise ValueError("quantized tensor is not a linear weight: " + key)
+    try:
+        layer = model.get_submodule(key[:-len(".weight")])
+    except AttributeError as exc:
+        raise ValueError("quantized linear layer is missing: " + key) from exc
+    shape = tuple(int(d) for d in reversed(np.asarray(tensor.shape).tolist()))
+    if not isinstance(layer, torch.nn.Linear) or shape != tuple(layer.weight.shape):
+        raise ValueError("quantized tensor does not match a linear layer: " + key)
+    return layer
 
 
 def replace_quantized_linear_layers(model, source, include_half=False):
-    """Replace all quantized linear weights after checking the complete mapping (tools/idol_packed.py:97-129).
-
-    `source` maps GGUF tensor names to source tensors. A quantized tensor that is not a linear weight is an error.
-    """
-    supported = {GGMLQuantizationType.Q8_0, GGMLQuantizationType.Q4_0, GGMLQuantizationType.Q2_K,
-                 GGMLQuantizationType.Q4_K, GGMLQuantizationType.Q6_K}
-    selected = {name: tensor for name, tensor in source.items()
-                if tensor.tensor_type in supported or
-                (include_half and tensor.tensor_type == GGMLQuantizationType.F16
-                 and len(tensor.shape) == 2 and name.endswith('.weight'))}
-    names = []
-    for key, tensor in selected.items():
-        if not key.endswith('.weight'):
-            raise ValueError('quantized tensor is not a linear weight: ' + key)
-        name = key[:-len('.weight')]
-        try:
-            module = model.get_submodule(name)
-        except AttributeError as exc:
-            raise ValueError('quantized linear layer is missing: ' + key) from exc
-        if (not isinstance(module, torch.nn.Linear)
-                or tuple(reversed(np.asarray(tensor.shape).tolist())) != tuple(module.weight.shape)):
-            raise ValueError('quantized tensor does not match a linear layer: ' + key)
-        names.append(name)
-    for name in names:
-        tensor = selected[name + '.weight']
-        module = model.get_submodule(name)
-        parent_name, _, leaf = name.rpartition(".")
-        parent = model.get_submodule(parent_name) if parent_name else model
-        setattr(parent, leaf, PackedLinear(tensor, module.bias).to(device=module.weight.device))
-    return [name + '.weight' for name in names]
+    """Swaps the nn.Linear layers whose weights `source` (GGUF tensor name -> tensor) holds packed for PackedLinear
+    layers on the same device, after every one of them has been checked; returns the weight names replaced (the
+    interface of tools/idol_packed.py:97-129)."""
+    plan = [(key, tensor, _target_layer(model, key, tensor)) for key, tensor in source.items()
+            if _replaceable(key, tensor, include_half)]
+    for key, tensor, layer in plan:
+        parent, _, leaf = key[:-len(".weight")].rpartition(".")
+        setattr(model.get_submodule(parent) if parent else model, leaf,
+                PackedLinear(tensor, layer.bias).to(device=layer.weight.device))
+    return [key for key, _, _ in plan]
