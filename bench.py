@@ -19,7 +19,10 @@ Also reported, in the same JSON line:
                  anchor) on 1024 anchors and 8192 latent tokens, fp32 activations, the reference's float-kernel
                  numerics, unless --no-decoders; with the reference's own decoders timed on the host beside them;
   decode_ms      Decoders.decode end to end: 262144 Gaussians (8192 anchors), octree descent to level 8
-  cpu_baseline   the reference's own CPU kernels (oracle/_ref, float kernel, all host cores) on the same MLP block
+  int8_*         the same block in INT8 mode (the reference's integer-kernel semantics on int8 MFMA), per GEMM
+  layernorm_*    idolq_layernorm at 8192 x 1536 bf16 over rotating buffers larger than the Infinity Cache (HBM GB/s)
+  cpu_baseline   the reference's own CPU kernels (oracle/_ref, float kernel, its OpenMP threads) on the same MLP block;
+                 cpu_baseline_int8 the same with its integer (AVX-VNNI) kernel
 """
 import argparse
 import json
@@ -57,10 +60,25 @@ def parse():
                    help="skip the real-size octree and Gaussian decoders (dim 1024, 16 heads, 4 + 16 blocks)")
     p.add_argument("--denoiser-layers", type=int, default=24)
     p.add_argument("--cpu-rows", type=int, default=1024, help="rows of the MLP block the CPU baseline runs")
+    p.add_argument("--counter-probe", action="store_true",
+                   help="launch only the MLP block's GEMMs in DEQUANT and INT8 mode and the config-2 self- and "
+                        "cross-attention, 3 times each, untimed: the program the rocprofv3 --pmc counter passes "
+                        "(MFMA busy cycles and ops, VALU instructions) run")
     p.add_argument("--traffic-probe", action="store_true",
                    help="launch only the calibration copy (512 MiB bf16) and the two GEMMs, 3 times each, untimed: the "
                         "program rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs to measure HBM bytes per launch")
     return p.parse_args()
+
+
+def cpu_threads():
+    """Threads the reference's OpenMP kernels run with: OMP_NUM_THREADS when set, else the cores this process may
+    run on (its affinity mask), which is libgomp's default."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return int(env) if env.isdigit() and int(env) > 0 else len(os.sched_getaffinity(0))
+
+
+def cpu_note():
+    return f"{cpu_threads()} OpenMP threads on {len(os.sched_getaffinity(0))} cores of the process's affinity mask"
 
 
 def mlp_inputs(torch, L, seed=0):
@@ -118,6 +136,35 @@ def run_traffic_probe(args):
         blk.down()
     torch.cuda.synchronize()
     print(json.dumps({"traffic_probe": "done", "copy_bytes": COPY_ROWS * COPY_COLS * 2}), flush=True)
+
+
+def run_counter_probe(args):
+    import torch
+    import idolq_lib as L
+
+    inputs = mlp_inputs(torch, L)
+    for mode in (L.MODE_DEQUANT, L.MODE_INT8):
+        blk = MlpBlock(torch, L, mode, inputs)
+        for _ in range(3):
+            blk.up()
+            blk.down()
+        torch.cuda.synchronize()
+        del blk
+    # config 2's attention: batch 2 x 4096 queries, 24 heads of 64; self over 4096 keys (q, k, v column slices of the
+    # [8192, 4608] projection), cross over 1024 context keys (k, v slices of the [2048, 3072] projection)
+    gen = torch.Generator(device="cuda").manual_seed(6)
+    B, S, Lc, heads, hd = 2, 4096, 1024, 24, 64
+    qkv = torch.randn((B * S, 3 * D), device="cuda", generator=gen).bfloat16()
+    kv = torch.randn((B * Lc, 2 * D), device="cuda", generator=gen).bfloat16()
+    out = torch.empty((B * S, D), device="cuda", dtype=torch.bfloat16)
+    for _ in range(3):
+        L.attention(qkv[:, :D], qkv[:, D:2 * D], qkv[:, 2 * D:], B, S, S, heads, hd, 3 * D, 3 * D, S * 3 * D,
+                    S * 3 * D, out, D, S * D)
+    for _ in range(3):
+        L.attention(qkv[:, :D], kv[:, :D], kv[:, D:], B, S, Lc, heads, hd, 3 * D, 2 * D, S * 3 * D, Lc * 2 * D,
+                    out, D, S * D)
+    torch.cuda.synchronize()
+    print(json.dumps({"counter_probe": "done"}), flush=True)
 
 
 def measured_traffic():
@@ -189,6 +236,72 @@ def run_gpu(args):
     }
     del blk
     return out, inputs
+
+
+def run_int8_block(args, inputs):
+    """The MLP block in INT8 mode (the reference's integer kernel semantics: activations quantized per row and
+    32-block, int8 MFMA block dots, per-block fp32 scale fold) on the same inputs: per-GEMM launch time from HIP
+    events on the launch stream (activation quantization included, it is part of the mode), as TFLOP/s-equivalent
+    and as a fraction of the int8 MFMA peak."""
+    import torch
+    import idolq_lib as L
+
+    blk = MlpBlock(torch, L, L.MODE_INT8, inputs)
+    for _ in range(3):
+        blk.up()
+        blk.down()
+    torch.cuda.synchronize()
+    steps = max(5, args.steps // 2)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    for e in evs:
+        e[0].record()
+        blk.up()
+        e[1].record()
+        blk.down()
+        e[2].record()
+    torch.cuda.synchronize()
+    up = sum(e[0].elapsed_time(e[1]) for e in evs) / steps
+    down = sum(e[1].elapsed_time(e[2]) for e in evs) / steps
+    flop = 2.0 * M * D * H
+    gemm_ms = (up + down) / 2
+    tops = flop / (gemm_ms * 1e-3) / 1e12
+    del blk
+    return {"int8_gemm_ms": round(gemm_ms, 4), "int8_gemm_ms_up": round(up, 4), "int8_gemm_ms_down": round(down, 4),
+            "int8_tops": round(tops, 1), "int8_pct_int8_peak": round(tops / PEAK_TFLOPS["int8"], 4)}
+
+
+LN_ROWS, LN_BUFFERS = 8192, 12  # 12 x (8192 x 1536 bf16 in + out) = 604 MB rotating, over twice the 256 MB cache
+
+
+def run_layernorm_hbm(args):
+    """idolq_layernorm on the denoiser's activation shape (8192 x 1536 bf16, adaLN) over LN_BUFFERS input/output
+    pairs used in turn, so successive calls miss the Infinity Cache: ms per call and GB/s of its 2 * rows * dim * 2
+    bytes against the 8 TB/s HBM peak."""
+    import torch
+    import idolq_lib as L
+
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    xs = [torch.randn((LN_ROWS, D), device="cuda", generator=gen).bfloat16() for _ in range(LN_BUFFERS)]
+    ys = [torch.empty_like(x) for x in xs]
+    shift = torch.randn((2, D), device="cuda", generator=gen) * 0.1
+    scale = torch.randn((2, D), device="cuda", generator=gen) * 0.1
+    for i in range(LN_BUFFERS):
+        L.layernorm(xs[i], 1e-6, shift=shift, scale=scale, rows_per_batch=LN_ROWS // 2, out=ys[i])
+    torch.cuda.synchronize()
+    reps = 5 * LN_BUFFERS
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for r in range(reps):
+        i = r % LN_BUFFERS
+        L.layernorm(xs[i], 1e-6, shift=shift, scale=scale, rows_per_batch=LN_ROWS // 2, out=ys[i])
+    stop.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / reps
+    nbytes = 2 * LN_ROWS * D * 2
+    return {"layernorm_ms": round(ms, 4), "layernorm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "layernorm_hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_GBS, 3),
+            "layernorm_config": f"{LN_ROWS} x {D} bf16 adaLN, {LN_BUFFERS} rotating buffer pairs "
+                                f"({LN_BUFFERS * nbytes / 1e6:.0f} MB)"}
 
 
 def run_denoiser(args):
@@ -409,9 +522,8 @@ def run_cpu_decoders():
             ref.close()
     oct_s = times[("oct", 1)] + 3 * (times[("oct", 2)] - times[("oct", 1)])
     gs_s = times[("gs", 1)] + 15 * (times[("gs", 2)] - times[("gs", 1)])
-    cores = int(os.environ.get("OMP_NUM_THREADS", 0)) or os.cpu_count()
     return {"decoders_cpu_oct_ms_est": round(oct_s * 1e3, 1), "decoders_cpu_gs_ms_est": round(gs_s * 1e3, 1),
-            "decoders_cpu_cores": cores,
+            "decoders_cpu_cores": cpu_threads(),
             "decoders_cpu_note": "reference idol::Decoders, float kernel, model width with 1 and 2 blocks timed "
                                  "(median of 3 after 1 warm-up), 4 + 16 blocks extrapolated from the per-block time"}
 
@@ -448,8 +560,7 @@ def run_cpu_decoder_mlp(model, sample=16384):
         run()
         times.append(time.perf_counter() - t0)
     t = float(np.median(times)) * DECODER_POINTS / sample
-    cores = int(os.environ.get("OMP_NUM_THREADS", 0)) or os.cpu_count()
-    return {"decoder_mlp_cpu_ms_est": round(t * 1e3, 2), "decoder_mlp_cpu_cores": cores,
+    return {"decoder_mlp_cpu_ms_est": round(t * 1e3, 2), "decoder_mlp_cpu_cores": cpu_threads(),
             "decoder_mlp_cpu_note": f"reference kernels.cpp float kernel (3 Q8_0 layers) + dense head on {sample} "
                                     f"points, median of 3 after 1 warm-up, scaled to {DECODER_POINTS} points"}
 
@@ -495,14 +606,18 @@ def run_cpu_denoiser_layer(model, ctx):
         f = O.ref_gelu_tanh(lin("up", O.ref_norm_rows(x, 1e-6)))
         return lin("down", f, residual=x)
 
-    t0 = time.perf_counter()
     one_layer(x)
-    t = time.perf_counter() - t0
-    cores = int(os.environ.get("OMP_NUM_THREADS", 0)) or os.cpu_count()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        one_layer(x)
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
     return {"denoiser_cpu_layer_ms": round(t * 1e3, 1), "denoiser_cpu_step_ms_est": round(24 * t * 1e3, 1),
-            "denoiser_cpu_cores": cores,
+            "denoiser_cpu_cores": cpu_threads(),
             "denoiser_cpu_note": "reference kernels.cpp float kernel + attention + norm_rows + gelu_tanh on one "
-                                 "full-size layer (batch 2 x 4096 tokens), step = 24 x layer"}
+                                 "full-size layer (batch 2 x 4096 tokens), median of 3 after 1 warm-up, step = 24 x "
+                                 "layer; " + cpu_note()}
 
 
 def run_cpu_baseline(args, inputs):
@@ -517,30 +632,46 @@ def run_cpu_baseline(args, inputs):
     wu, wd = w_up.cpu().numpy(), w_down.cpu().numpy()
     bu, bd = b_up.cpu().numpy(), b_down.cpu().numpy()
     kind = "reference" if O.ref_available() else "port"
+    flop = 2 * 2.0 * rows * D * H
+
+    def timed(block):
+        block()
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            block()
+            times.append(time.perf_counter() - t0)
+        return float(np.median(times))
+
+    def result(t, what):
+        return {"value": flop / t / 1e12, "unit": "TFLOP/s", "cores": cpu_threads(), "kind": kind,
+                "sample": f"MLP block (up + tanh-GELU + down + residual) on {rows} of {M} rows, fp32, {what}, median "
+                          f"of 3 after 1 warm-up, {t * 1e3:.1f} ms per block; {cpu_note()}"}
+
     if kind == "reference":
         blob_up, blob_down = O.q8_0_to_panel(wu, H, D), O.q8_0_to_panel(wd, D, H)
 
-        def block():
-            hh = O.ref_gemm_panel(xs, blob_up, bu, H, D, mode=0)
+        def block(mode):
+            hh = O.ref_gemm_panel(xs, blob_up, bu, H, D, mode=mode)
             hh = O.ref_gelu_tanh(hh)
-            return O.ref_gemm_panel(hh, blob_down, bd, D, H, residual=xs, mode=0)
-    else:
-        def block():
-            hh = O.gelu_tanh(O.gemm_q8_float(xs, wu, H, D, bu))
-            return O.gemm_q8_float(hh, wd, D, H, bd, residual=xs)
+            return O.ref_gemm_panel(hh, blob_down, bd, D, H, residual=xs, mode=mode)
 
-    block()
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        block()
-        times.append(time.perf_counter() - t0)
-    t = float(np.median(times))
-    flop = 2 * 2.0 * rows * D * H
-    cores = int(os.environ.get("OMP_NUM_THREADS", 0)) or os.cpu_count()
-    return {"value": flop / t / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": kind,
-            "sample": f"MLP block (up + tanh-GELU + down + residual) on {rows} of {M} rows, fp32, float kernel "
-                      f"(IDOL_QUANT_KERNEL=float), median of 3 after 1 warm-up, {t * 1e3:.1f} ms per block"}
+        out = result(timed(lambda: block(0)), "float kernel (IDOL_QUANT_KERNEL=float)")
+        if O.ref_int8_supported():
+            out8 = result(timed(lambda: block(1)), "integer kernel (AVX-VNNI vpdpbusd, the reference's default "
+                                                   "where the host has avxvnni)")
+        else:
+            out8 = {"value": None, "unit": "TFLOP/s", "kind": kind,
+                    "sample": "absent: this host has no avxvnni, so the reference build has no integer kernel"}
+        return out, out8
+
+    def port_block():
+        hh = O.gelu_tanh(O.gemm_q8_float(xs, wu, H, D, bu))
+        return O.gemm_q8_float(hh, wd, D, H, bd, residual=xs)
+
+    out = result(timed(port_block), "the oracle's scalar restatement of the float kernel")
+    out["cores"] = 1
+    return out, {"value": None, "unit": "TFLOP/s", "kind": "port", "sample": "absent: no reference build"}
 
 
 def main():
@@ -550,6 +681,9 @@ def main():
         sys.exit(2)
     if args.traffic_probe:
         run_traffic_probe(args)
+        return
+    if args.counter_probe:
+        run_counter_probe(args)
         return
     gpu, inputs = run_gpu(args)
     result = {
@@ -571,6 +705,9 @@ def main():
         "roofline": gpu["roofline"],
         "pct_int8_peak": round(gpu["pct_int8_peak"], 4),
     }
+    if args.mode == "dequant":
+        result.update(run_int8_block(args, inputs))
+    result.update(run_layernorm_hbm(args))
     dec_model = None
     if not args.no_decoder_mlp:
         dec, dec_model = run_decoder_mlp(args)
@@ -583,7 +720,7 @@ def main():
         dn, model, ctx = run_denoiser(args)
         result.update(dn)
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = run_cpu_baseline(args, inputs)
+        result["cpu_baseline"], result["cpu_baseline_int8"] = run_cpu_baseline(args, inputs)
         if model is not None:
             cpu = run_cpu_denoiser_layer(model, ctx)
             result.update(cpu)
