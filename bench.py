@@ -21,6 +21,7 @@ Also reported, in the same JSON line:
   decode_ms      Decoders.decode end to end: 262144 Gaussians (8192 anchors), octree descent to level 8
   int8_*         the same block in INT8 mode (the reference's integer-kernel semantics on int8 MFMA), per GEMM
   layernorm_*    idolq_layernorm at 8192 x 1536 bf16 over rotating buffers larger than the Infinity Cache (HBM GB/s)
+  gemv_*         the small-m form at m = 1 and 16 on 4096 x 4096 Q8_0 weights rotating over 428 MB (HBM GB/s)
   cpu_baseline   the reference's own CPU kernels (oracle/_ref, float kernel, its OpenMP threads) on the same MLP block;
                  cpu_baseline_int8 the same with its integer (AVX-VNNI) kernel
 """
@@ -270,6 +271,20 @@ def run_int8_block(args, inputs):
             "int8_tops": round(tops, 1), "int8_pct_int8_peak": round(tops / PEAK_TFLOPS["int8"], 4)}
 
 
+def gpu_time_us(torch, fn, reps):
+    """Average GPU microseconds of fn() over `reps` back-to-back calls. The calls are queued behind a GPU spin long
+    enough for the host to enqueue all of them, so the events time the GPU's work, not the host's call overhead."""
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(int(2e6 + reps * 1e5))  # clock cycles: ~1 ms + 40 us per call at 2.4 GHz
+    start.record()
+    for _ in range(reps):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / reps * 1e3
+
+
 LN_ROWS, LN_BUFFERS = 8192, 12  # 12 x (8192 x 1536 bf16 in + out) = 604 MB rotating, over twice the 256 MB cache
 
 
@@ -285,23 +300,57 @@ def run_layernorm_hbm(args):
     ys = [torch.empty_like(x) for x in xs]
     shift = torch.randn((2, D), device="cuda", generator=gen) * 0.1
     scale = torch.randn((2, D), device="cuda", generator=gen) * 0.1
-    for i in range(LN_BUFFERS):
+    turn = [0]
+
+    def call():
+        i = turn[0] % LN_BUFFERS
+        turn[0] += 1
         L.layernorm(xs[i], 1e-6, shift=shift, scale=scale, rows_per_batch=LN_ROWS // 2, out=ys[i])
-    torch.cuda.synchronize()
-    reps = 5 * LN_BUFFERS
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for r in range(reps):
-        i = r % LN_BUFFERS
-        L.layernorm(xs[i], 1e-6, shift=shift, scale=scale, rows_per_batch=LN_ROWS // 2, out=ys[i])
-    stop.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(stop) / reps
+
+    for _ in range(LN_BUFFERS):
+        call()
+    ms = gpu_time_us(torch, call, 5 * LN_BUFFERS) * 1e-3
     nbytes = 2 * LN_ROWS * D * 2
     return {"layernorm_ms": round(ms, 4), "layernorm_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
             "layernorm_hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_GBS, 3),
             "layernorm_config": f"{LN_ROWS} x {D} bf16 adaLN, {LN_BUFFERS} rotating buffer pairs "
                                 f"({LN_BUFFERS * nbytes / 1e6:.0f} MB)"}
+
+
+GEMV_N, GEMV_K, GEMV_SETS = 4096, 4096, 24  # 24 x 17.8 MB of Q8_0 weights (428 MB), over the 256 MB Infinity Cache
+
+
+def run_gemv_hbm(args):
+    """The small-m form (q8_gemv_kernel) at m = 1 and m = 16, bf16 x, DEQUANT, on GGUF row-major Q8_0 weights
+    [4096 x 4096] taken in turn from GEMV_SETS matrices: us per call and GB/s of the bytes a call must move (weights,
+    activations, output) against the 8 TB/s HBM peak."""
+    import torch
+    import idolq_lib as L
+
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    ws = [L.quantize_q8_0(torch.randn((GEMV_N, GEMV_K), device="cuda", generator=gen) * 0.02)
+          for _ in range(GEMV_SETS)]
+    out = {}
+    for m in (1, 16):
+        x = torch.randn((m, GEMV_K), device="cuda", generator=gen).bfloat16()
+        y = torch.empty((m, GEMV_N), device="cuda", dtype=torch.bfloat16)
+        turn = [0]
+
+        def call():
+            L.gemm(x, ws[turn[0] % GEMV_SETS], GEMV_N, mode=L.MODE_DEQUANT, out=y)
+            turn[0] += 1
+
+        for _ in range(GEMV_SETS):
+            call()
+        us = gpu_time_us(torch, call, 4 * GEMV_SETS)
+        nbytes = GEMV_N * GEMV_K // 32 * 34 + m * GEMV_K * 2 + m * GEMV_N * 2
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out.update({f"gemv_m{m}_us": round(us, 2), f"gemv_m{m}_gbs": round(gbs, 1),
+                    f"gemv_m{m}_hbm_frac": round(gbs / HBM_GBS, 3)})
+    out["gemv_config"] = (f"Q8_0 [{GEMV_N} x {GEMV_K}] row-major GGUF blocks, bf16 x, DEQUANT, {GEMV_SETS} weight "
+                          f"matrices in turn ({GEMV_SETS * GEMV_N * GEMV_K // 32 * 34 / 1e6:.0f} MB)")
+    del ws
+    return out
 
 
 def run_denoiser(args):
@@ -708,6 +757,7 @@ def main():
     if args.mode == "dequant":
         result.update(run_int8_block(args, inputs))
     result.update(run_layernorm_hbm(args))
+    result.update(run_gemv_hbm(args))
     dec_model = None
     if not args.no_decoder_mlp:
         dec, dec_model = run_decoder_mlp(args)

@@ -64,4 +64,10 @@ bool wide_eligible(const GemmParams& p, int xt, int mode);
 size_t wide_workspace_bytes();
 int launch_wide(GemmParams p, int xt, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+// The small-m form (q8_gemv.hip): m <= kGemvMaxRows activation rows on GGUF row-major weights (k % 256 == 0, 16-byte
+// aligned), DEQUANT on 16-bit activations or EXACT; 16 weight rows per workgroup, the depth split over 8 waves.
+constexpr int kGemvMaxRows = 16;
+bool gemv_eligible(const GemmParams& p, int xt, int mode);
+int launch_gemv(GemmParams p, int xt, int mode, hipStream_t stream);
+
 }  // namespace idolq

@@ -861,7 +861,9 @@ extern "C" int idolq_q8_0_gemm(const void* x, int x_dtype, int64_t m, int64_t k,
         return launch_int8<128, 128, false>(p, w4, s);
     }
     const int xt = x_dtype == IDOLQ_BF16 ? XT_BF16 : x_dtype == IDOLQ_F16 ? XT_F16 : XT_F32;
-    return launch_16bit(p, xt, mode == IDOLQ_MODE_DEQUANT ? MODE_DEQUANT : MODE_EXACT, w4, workspace, workspace_bytes, s);
+    const int kmode = mode == IDOLQ_MODE_DEQUANT ? MODE_DEQUANT : MODE_EXACT;
+    if (gemv_eligible(p, xt, kmode)) return launch_gemv(p, xt, kmode, s);
+    return launch_16bit(p, xt, kmode, w4, workspace, workspace_bytes, s);
 }
 
 extern "C" int idolq_q8_0_block_dots(const int8_t* qa, int64_t m, int64_t k, const uint8_t* w, int64_t n_total,
