@@ -65,16 +65,23 @@ struct WideSplit {
     int* count;   // G counters, zero between launches (the workspace's first bytes)
 };
 
-template <int RT, int CT>
+// Q4K: the weights are GGUF Q4_K super-blocks, row-major (one row: k / 256 blocks of 144 bytes: fp16 d, fp16 dmin,
+// 12 bytes of 6-bit scales and minimums, 128 bytes of nibbles); a 64-deep stage is the 32-groups 2 j and 2 j + 1 of a
+// super-block (j = stage % 4), whose codes are the low and the high nibbles of the same 32 bytes 16 + 32 j .. of the
+// block. Per 32-row group and stage a wave loads those 32 bytes of each row (1 KB, lane l: row l % 32, bytes
+// 16 (l / 32) .. + 15) and the rows' 16-byte headers (512 bytes), straight from the row-major bytes.
+template <int RT, int CT, bool Q4K = false>
 struct WideCfg {
     static constexpr int BM = 32 * RT, BN = 128 * CT;
     static constexpr int ABuf = BM * 128;            // one stage of activations: BM rows x 64 16-bit values
-    static constexpr int WWave = CT * (2048 + 128);  // one stage of one wave's weight groups: codes, then scales
+    static constexpr int WCode = Q4K ? 1024 : 2048;  // one 32-row group's codes per stage
+    static constexpr int WScale = Q4K ? 512 : 128;   // and its scales (Q4_K: the super-block headers)
+    static constexpr int WWave = CT * (WCode + WScale);  // one stage of one wave's weight groups: codes, then scales
     static constexpr int WBuf = 4 * WWave;
     static constexpr int WBase = 3 * ABuf;
     static constexpr int Lds = WBase + 3 * WBuf;
     static constexpr int DA = BM / 32;               // activation loads (1 KB each) per wave per stage
-    static constexpr int DW = 2 * CT + 1;            // weight loads per wave per stage
+    static constexpr int DW = Q4K ? 2 * CT : 2 * CT + 1;  // weight loads per wave per stage
     static_assert(Lds <= 163840, "LDS budget");
 };
 
@@ -88,9 +95,44 @@ __device__ __forceinline__ void static_for(F&& f) {
     static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-template <typename T, int RT, int CT, int ACT, bool FAST, bool SPLIT>
+// (d * sc, dmin * m) of the 32-groups 2 pair and 2 pair + 1 of a Q4_K super-block from its 16-byte header (bytes 0-1
+// d, 2-3 dmin, 4-15 the 6-bit scales and minimums s[0..11]): for group j < 4, sc = s[j] & 63, m = s[4 + j] & 63; for
+// j >= 4, sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4), m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4). The products are
+// exact in fp32 (11-bit by 6-bit).
+__device__ __forceinline__ void q4k_header(uint4 hd, int pair, float (&ab)[4]) {
+    const float d = half_bits_to_float((uint16_t)(hd.x & 0xffff)), dmin = half_bits_to_float((uint16_t)(hd.x >> 16));
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int j = 2 * pair + t;
+        uint32_t sc, mn;
+        if (j < 4) {
+            sc = (hd.y >> (8 * j)) & 63;
+            mn = (hd.z >> (8 * j)) & 63;
+        } else {
+            const int jj = j - 4;
+            const uint32_t c = (hd.w >> (8 * jj)) & 0xff;
+            sc = (c & 15) | (((hd.y >> (8 * jj + 6)) & 3) << 4);
+            mn = (c >> 4) | (((hd.z >> (8 * jj + 6)) & 3) << 4);
+        }
+        ab[2 * t] = d * (float)sc;
+        ab[2 * t + 1] = dmin * (float)mn;
+    }
+}
+
+// Four Q4_K codes (0..15, one per byte) to four operands T((d * sc) * q - dmin * m) = T(a * q - b); the product is
+// exact, so one rounding before the conversion, as the reference's expansion.
+template <typename T>
+__device__ __forceinline__ uint2 q4k_dequant4(uint32_t nibbles, float a, float b) {
+    typedef typename PipeMfma<T>::pair T2;
+    const f32x2 lo = {(float)(nibbles & 0xff), (float)((nibbles >> 8) & 0xff)};
+    const f32x2 hi = {(float)((nibbles >> 16) & 0xff), (float)(nibbles >> 24)};
+    return make_uint2(__builtin_bit_cast(uint32_t, __builtin_convertvector(lo * a - b, T2)),
+                      __builtin_bit_cast(uint32_t, __builtin_convertvector(hi * a - b, T2)));
+}
+
+template <typename T, int RT, int CT, int ACT, bool FAST, bool SPLIT, bool Q4K = false>
 __global__ __launch_bounds__(kWideThreads) void q8_wide_kernel(GemmParams p, WideSplit sp) {
-    typedef WideCfg<RT, CT> C;
+    typedef WideCfg<RT, CT, Q4K> C;
     typedef typename PipeMfma<T>::vec Vec;
     typedef typename PipeMfma<T>::pair T2;
     constexpr int DA = C::DA, DW = C::DW;
@@ -107,20 +149,32 @@ __global__ __launch_bounds__(kWideThreads) void q8_wide_kernel(GemmParams p, Wid
     // ---- per-tile load offsets (bytes, 32-bit)
     // activations: load j of this wave fills LDS 16-byte chunks u = 64 (DA wave + j) + lane of the stage buffer:
     // row u / 8, position u % 8, holding chunk (u % 8) ^ ((row >> 1) & 7) of the row
-    uint32_t a_off[DA], w_off[CT], ws_off;
+    uint32_t a_off[DA], w_off[CT], ws_off, wh_off[CT];
+    int seg_k0 = 0;  // Q4K: the segment's first stage (the stage's super-block and 32-group pair follow from it)
     auto start_tile = [&](int m0, int n0, int k0) __attribute__((always_inline)) {
         xg = uniform_ptr(static_cast<const char*>(p.x) + (size_t)k0 * 128);
-        wg = uniform_ptr(reinterpret_cast<const char*>(p.w) + (size_t)k0 * kGroupBytes);
+        wg = uniform_ptr(reinterpret_cast<const char*>(p.w) + (Q4K ? 0 : (size_t)k0 * kGroupBytes));
+        seg_k0 = k0;
 #pragma unroll
         for (int j = 0; j < DA; ++j) {
             const int u = (wave * DA + j) * 64 + lane, row = u >> 3, c = (u & 7) ^ ((row >> 1) & 7);
             a_off[j] = (uint32_t)((int64_t)min(m0 + row, p.m - 1) * p.ldx * 2 + c * 16);
         }
-        const int g0 = n0 / 32 + wave * CT;
+        if constexpr (Q4K) {
+            // rows past the window read its last row (their outputs are never stored)
 #pragma unroll
-        for (int c = 0; c < CT; ++c) w_off[c] = (uint32_t)(min(g0 + c, p.groups - 1) * gstride + 16 * lane);
-        // scales: lanes 8 c .. 8 c + 7 fetch the 128 bytes of group c
-        ws_off = (uint32_t)(min(g0 + min(lane >> 3, CT - 1), p.groups - 1) * gstride + 2048 + 16 * (lane & 7));
+            for (int c = 0; c < CT; ++c) {
+                const int row0 = n0 + 32 * (wave * CT + c);
+                w_off[c] = (uint32_t)((int64_t)min(row0 + (lane & 31), p.groups - 1) * p.row_bytes + 16 * (lane >> 5));
+                wh_off[c] = (uint32_t)((int64_t)min(row0 + (lane & 31), p.groups - 1) * p.row_bytes);
+            }
+        } else {
+            const int g0 = n0 / 32 + wave * CT;
+#pragma unroll
+            for (int c = 0; c < CT; ++c) w_off[c] = (uint32_t)(min(g0 + c, p.groups - 1) * gstride + 16 * lane);
+            // scales: lanes 8 c .. 8 c + 7 fetch the 128 bytes of group c
+            ws_off = (uint32_t)(min(g0 + min(lane >> 3, CT - 1), p.groups - 1) * gstride + 2048 + 16 * (lane & 7));
+        }
     };
     // load j < DA of this wave's share of activation stage s
     auto issue_a_piece = [&](int s, int j) __attribute__((always_inline)) {
@@ -132,12 +186,22 @@ __global__ __launch_bounds__(kWideThreads) void q8_wide_kernel(GemmParams p, Wid
     };
     // load i < DW of this wave's weight stage s: block i % 2 of group i / 2, then (i = 2 CT) the scales
     auto issue_w_piece = [&](int s, int i) __attribute__((always_inline)) {
-        const char* base = wg + (size_t)s * kGroupBytes;
         const uint32_t dst = lds0 + C::WBase + (s % 3) * C::WBuf + wave * C::WWave;
-        if (i < 2 * CT)
-            lds_dma16(base + (i & 1) * 1024, w_off[i >> 1], dst + (i >> 1) * 2048 + (i & 1) * 1024);
-        else if (lane < 8 * CT)
-            lds_dma16(base, ws_off, dst + CT * 2048);
+        if constexpr (Q4K) {
+            // stage seg_k0 + s: super-block (seg_k0 + s) / 4, nibble bytes 16 + 32 ((seg_k0 + s) % 4) .. + 31
+            const int as = seg_k0 + s;
+            const char* sb = wg + (size_t)(as >> 2) * 144;
+            if (i < CT)
+                lds_dma16(sb + 16 + 32 * (as & 3), w_off[i], dst + i * 1024);
+            else if (lane < 32)
+                lds_dma16(sb, wh_off[i - CT], dst + CT * 1024 + (i - CT) * 512);
+        } else {
+            const char* base = wg + (size_t)s * kGroupBytes;
+            if (i < 2 * CT)
+                lds_dma16(base + (i & 1) * 1024, w_off[i >> 1], dst + (i >> 1) * 2048 + (i & 1) * 1024);
+            else if (lane < 8 * CT)
+                lds_dma16(base, ws_off, dst + CT * 2048);
+        }
     };
     auto issue_w = [&](int s) __attribute__((always_inline)) {
 #pragma unroll
@@ -151,30 +215,56 @@ __global__ __launch_bounds__(kWideThreads) void q8_wide_kernel(GemmParams p, Wid
     for (int j = 0; j < 4; ++j) x_lane[j] = (lane & 31) * 128 + (((2 * j + (lane >> 5)) ^ ((lane >> 1) & 7)) * 16);
     Vec xo[2][RT];     // x operands of two steps
     uint4 wq[2][CT];   // weight operands of two steps (bits of Vec)
-    uint4 rc[CT][2];   // this stage's codes: group c, block b (two MFMA steps each)
+    uint4 rc[CT][2];   // this stage's codes: group c, block b (two MFMA steps each); Q4K: rc[c][0] only
     uint32_t rs[CT];   // this stage's scales: group c, block 0 low / block 1 high
+    float rab[CT][4];  // Q4K: (d * sc, dmin * m) of the stage's two 32-groups, for group c
     f32x16 acc[RT][CT];
 
     auto read_x1 = [&](int buf, int j, int set, int rt) __attribute__((always_inline)) {
         xo[set][rt] = *reinterpret_cast<const Vec*>(smem + buf * C::ABuf + x_lane[j] + rt * 4096);
     };
     // piece c < CT: the codes of group c; piece CT: the scales of every group
-    auto read_raw_piece = [&](int buf, int c) __attribute__((always_inline)) {
+    // stage: the segment stage whose bytes buffer buf holds (Q4K: its 32-group pair is (seg_k0 + stage) % 4)
+    auto read_raw_piece = [&](int buf, int c, int stage) __attribute__((always_inline)) {
         const char* wb = smem + C::WBase + buf * C::WBuf + wave * C::WWave;
-        if (c < CT) {
+        if constexpr (Q4K) {
+            if (c < CT) {
+                // row lane % 32: nibble bytes 8 h .. 8 h + 7 (steps 0 and 2) and 16 + 8 h .. (steps 1 and 3)
+                const int r = lane & 31, h = lane >> 5;
+                const uint2 lo = *reinterpret_cast<const uint2*>(wb + c * 1024 + 16 * r + 8 * h);
+                const uint2 hi = *reinterpret_cast<const uint2*>(wb + c * 1024 + 16 * (32 + r) + 8 * h);
+                rc[c][0] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+            } else {
 #pragma unroll
-            for (int b = 0; b < 2; ++b) rc[c][b] = *reinterpret_cast<const uint4*>(wb + c * 2048 + b * 1024 + 16 * lane);
+                for (int g = 0; g < CT; ++g) {
+                    const uint4 hd = *reinterpret_cast<const uint4*>(wb + CT * 1024 + g * 512 + 16 * (lane & 31));
+                    q4k_header(hd, (seg_k0 + stage) & 3, rab[g]);
+                }
+            }
         } else {
+            if (c < CT) {
 #pragma unroll
-            for (int g = 0; g < CT; ++g) rs[g] = *reinterpret_cast<const uint32_t*>(wb + CT * 2048 + g * 128 + 4 * (lane & 31));
+                for (int b = 0; b < 2; ++b) rc[c][b] = *reinterpret_cast<const uint4*>(wb + c * 2048 + b * 1024 + 16 * lane);
+            } else {
+#pragma unroll
+                for (int g = 0; g < CT; ++g) rs[g] = *reinterpret_cast<const uint32_t*>(wb + CT * 2048 + g * 128 + 4 * (lane & 31));
+            }
         }
     };
     // slice k < 2 CT of step j's weight operands: four codes (half k % 2 of group k / 2) to T(fp32(d) * q)
     auto convert_slice = [&](int j, int set, int k) __attribute__((always_inline)) {
         const int c = k >> 1, h = k & 1, b = j >> 1;
-        const float d = half_bits_to_float((uint16_t)(rs[c] >> (16 * b)));
-        const uint4 q = rc[c][b];
-        const uint2 o = dequant4<T>((j & 1) ? (h ? q.w : q.z) : (h ? q.y : q.x), d);
+        uint2 o;
+        if constexpr (Q4K) {
+            // step j: 32-group b = j / 2 of the pair (low nibbles for b = 0, high for b = 1), bytes of piece j % 2
+            const uint4 q = rc[c][0];
+            const uint32_t word = (j & 1) ? (h ? q.w : q.z) : (h ? q.y : q.x);
+            o = q4k_dequant4<T>(b ? (word >> 4) & 0x0f0f0f0fu : word & 0x0f0f0f0fu, rab[c][2 * b], rab[c][2 * b + 1]);
+        } else {
+            const float d = half_bits_to_float((uint16_t)(rs[c] >> (16 * b)));
+            const uint4 q = rc[c][b];
+            o = dequant4<T>((j & 1) ? (h ? q.w : q.z) : (h ? q.y : q.x), d);
+        }
         if (h) {
             wq[set][c].z = o.x;
             wq[set][c].w = o.y;
@@ -217,13 +307,13 @@ __global__ __launch_bounds__(kWideThreads) void q8_wide_kernel(GemmParams p, Wid
     };
     // step 3 and the first operands of the next stage (buffers nb): its weight bytes, x operands and the conversion
     // of its first weight operands; with ISSUE_A the activation loads of stage as go out in the first slots
-    auto step3_next = [&](int nb, auto issue_a_tag, int as) __attribute__((always_inline)) {
+    auto step3_next = [&](int nb, auto issue_a_tag, int as, int next) __attribute__((always_inline)) {
         run_step(1, [&](int i) __attribute__((always_inline)) {
             if constexpr (decltype(issue_a_tag)::value) {
                 if (i < DA) issue_a_piece(as, i);
             }
             if (i <= CT)
-                read_raw_piece(nb, i);
+                read_raw_piece(nb, i, next);
             else if (i <= CT + RT)
                 read_x1(nb, 0, 0, i - CT - 1);
             if (i >= CV) convert_slice(0, 0, i - CV);
@@ -376,7 +466,7 @@ __global__ __launch_bounds__(kWideThreads) void q8_wide_kernel(GemmParams p, Wid
             wait_vm<0>();
         __syncthreads();
 #pragma unroll
-        for (int c = 0; c <= CT; ++c) read_raw_piece(0, c);
+        for (int c = 0; c <= CT; ++c) read_raw_piece(0, c, 0);
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) read_x1(0, 0, 0, rt);
 #pragma unroll
@@ -389,20 +479,20 @@ __global__ __launch_bounds__(kWideThreads) void q8_wide_kernel(GemmParams p, Wid
             steps012(s % 3, issue, s + 2);
             wait_vm<DA + DW>();  // W(s + 1): A(s + 2), W(s + 2) may remain
             __syncthreads();
-            step3_next((s + 1) % 3, issue, s + 3);
+            step3_next((s + 1) % 3, issue, s + 3, s + 1);
         }
         if (s + 3 == S) {  // W(s + 2) is the last weight stage; no more activation loads
             steps012(s % 3, issue, s + 2);
             wait_vm<DA + DW>();
             __syncthreads();
-            step3_next((s + 1) % 3, no_issue, 0);
+            step3_next((s + 1) % 3, no_issue, 0, s + 1);
             ++s;
         }
         if (s + 2 == S) {  // nothing issued after W(s + 1)
             steps012(s % 3, no_issue, 0);
             wait_vm<0>();
             __syncthreads();
-            step3_next((s + 1) % 3, no_issue, 0);
+            step3_next((s + 1) % 3, no_issue, 0, s + 1);
             ++s;
         }
         // last stage
@@ -531,7 +621,7 @@ __global__ __launch_bounds__(kWideThreads) void q8_wide_kernel(GemmParams p, Wid
     }
 }
 
-template <typename T, int RT, int CT, bool SPLIT>
+template <typename T, int RT, int CT, bool SPLIT, bool Q4K>
 int launch_wide_s(GemmParams p, const WideSplit& sp, hipStream_t stream) {
     const dim3 grid(sp.G), block(kWideThreads);
     p.tiles_m = (p.m + 32 * RT - 1) / (32 * RT);
@@ -542,24 +632,30 @@ int launch_wide_s(GemmParams p, const WideSplit& sp, hipStream_t stream) {
                       (p.act == IDOLQ_ACT_NONE || p.act == IDOLQ_ACT_GELU_TANH || p.act == IDOLQ_ACT_RELU);
     // the register epilogue's activation is a template argument; other activations take the general path
     if (!fast)
-        hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, IDOLQ_ACT_NONE, false, SPLIT>), grid, block, 0, stream, p, sp);
+        hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, IDOLQ_ACT_NONE, false, SPLIT, Q4K>), grid, block, 0, stream, p, sp);
     else if (p.act == IDOLQ_ACT_GELU_TANH)
-        hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, IDOLQ_ACT_GELU_TANH, true, SPLIT>), grid, block, 0, stream, p, sp);
+        hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, IDOLQ_ACT_GELU_TANH, true, SPLIT, Q4K>), grid, block, 0, stream, p, sp);
     else if (p.act == IDOLQ_ACT_RELU)
-        hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, IDOLQ_ACT_RELU, true, SPLIT>), grid, block, 0, stream, p, sp);
+        hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, IDOLQ_ACT_RELU, true, SPLIT, Q4K>), grid, block, 0, stream, p, sp);
     else
-        hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, IDOLQ_ACT_NONE, true, SPLIT>), grid, block, 0, stream, p, sp);
+        hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, IDOLQ_ACT_NONE, true, SPLIT, Q4K>), grid, block, 0, stream, p, sp);
     return check_launch("q8_wide_kernel");
 }
 
 // Workspace: tile counters in the first kCountBytes, then the partial tiles.
 constexpr size_t kCountBytes = 4096;
 
-// The columns [n0, n0 + n) of a launch (multiples of 32).
+// The columns [n0, n0 + n) of a launch (multiples of 32). Q4K: p.groups counts weight rows (row-major blocks).
+template <bool Q4K>
 GemmParams column_window(GemmParams p, int n0, int n) {
     const int S = p.k / 64;
-    p.w += (size_t)(n0 / 32) * S * kGroupBytes;
-    p.groups -= n0 / 32;
+    if (Q4K) {
+        p.w += (size_t)n0 * p.row_bytes;
+        p.groups -= n0;
+    } else {
+        p.w += (size_t)(n0 / 32) * S * kGroupBytes;
+        p.groups -= n0 / 32;
+    }
     if (p.bias) p.bias = static_cast<const char*>(p.bias) + (size_t)n0 * dtype_size(p.bias_dt);
     if (p.res) p.res = static_cast<const char*>(p.res) + (size_t)n0 * dtype_size(p.res_dt);
     p.y = static_cast<char*>(p.y) + (size_t)n0 * dtype_size(p.y_dt);
@@ -575,7 +671,7 @@ GemmParams column_window(GemmParams p, int n0, int n) {
 //     (fills the CUs when 256-row tiles would leave a partial round);
 //   128-row tiles with stream-K over the tiles left after the whole rounds (a workspace is needed; about 6 more for
 //     the partial tiles). 256-row tiles are not split: their splits lose the L2 sharing of neighbouring workgroups.
-template <typename T>
+template <typename T, bool Q4K>
 int launch_wide_dtype(GemmParams p, void* workspace, size_t workspace_bytes, hipStream_t stream) {
     const long cus = cu_count(), S = p.k / 64;
     const long tm8 = (p.m + 255) / 256, tm4 = (p.m + 127) / 128, tn = (p.n + 255) / 256;
@@ -597,18 +693,18 @@ int launch_wide_dtype(GemmParams p, void* workspace, size_t workspace_bytes, hip
     const WideSplit none{0, 0, 0, 0, nullptr, nullptr};
     auto whole = [&](long tiles) { WideSplit sp = none; sp.G = (int)std::min(tiles, cus); return sp; };
     switch (plan) {
-        case 0: return launch_wide_s<T, 8, 2, false>(p, whole(tm8 * tn), stream);
-        case 1: return launch_wide_s<T, 4, 2, false>(p, whole(tm4 * tn), stream);
+        case 0: return launch_wide_s<T, 8, 2, false, Q4K>(p, whole(tm8 * tn), stream);
+        case 1: return launch_wide_s<T, 4, 2, false, Q4K>(p, whole(tm4 * tn), stream);
         case 2: {
             const int n1 = (int)cb8 * 256;
-            int rc = launch_wide_s<T, 8, 2, false>(column_window(p, 0, n1), whole(tm8 * cb8), stream);
+            int rc = launch_wide_s<T, 8, 2, false, Q4K>(column_window<Q4K>(p, 0, n1), whole(tm8 * cb8), stream);
             if (rc) return rc;
-            return launch_wide_s<T, 4, 2, false>(column_window(p, n1, p.n - n1), whole(tm4 * (tn - cb8)), stream);
+            return launch_wide_s<T, 4, 2, false, Q4K>(column_window<Q4K>(p, n1, p.n - n1), whole(tm4 * (tn - cb8)), stream);
         }
         default: {
             WideSplit sp{(int)cus, (int)dp4, (int)(units / cus), (int)(units % cus),
                          reinterpret_cast<float*>(static_cast<char*>(workspace) + kCountBytes), static_cast<int*>(workspace)};
-            return launch_wide_s<T, 4, 2, true>(p, sp, stream);
+            return launch_wide_s<T, 4, 2, true, Q4K>(p, sp, stream);
         }
     }
 }
@@ -624,15 +720,75 @@ bool wide_eligible(const GemmParams& p, int xt, int mode) {
 
 size_t wide_workspace_bytes() { return kCountBytes + (size_t)2 * cu_count() * 128 * 256 * 4; }
 
-int launch_wide(GemmParams p, int xt, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+namespace {
+template <bool Q4K>
+int launch_wide_any(GemmParams p, int xt, void* workspace, size_t workspace_bytes, hipStream_t stream) {
     // 4-element groups of y, the residual and the bias are vector-accessible
     int vec4 = reinterpret_cast<uintptr_t>(p.y) % (4 * dtype_size(p.y_dt)) == 0 && p.ldy % 4 == 0;
     if (p.res) vec4 = vec4 && reinterpret_cast<uintptr_t>(p.res) % (4 * dtype_size(p.res_dt)) == 0 && p.ldr % 4 == 0;
     if (p.bias) vec4 = vec4 && reinterpret_cast<uintptr_t>(p.bias) % (4 * dtype_size(p.bias_dt)) == 0;
     p.y_vec4 = vec4;
     if (workspace && reinterpret_cast<uintptr_t>(workspace) % 256 != 0) workspace = nullptr;
-    if (xt == XT_BF16) return launch_wide_dtype<__bf16>(p, workspace, workspace_bytes, stream);
-    return launch_wide_dtype<_Float16>(p, workspace, workspace_bytes, stream);
+    if (xt == XT_BF16) return launch_wide_dtype<__bf16, Q4K>(p, workspace, workspace_bytes, stream);
+    return launch_wide_dtype<_Float16, Q4K>(p, workspace, workspace_bytes, stream);
+}
+}  // namespace
+
+int launch_wide(GemmParams p, int xt, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    return launch_wide_any<false>(p, xt, workspace, workspace_bytes, stream);
 }
 
 }  // namespace idolq
+
+using namespace idolq;
+
+extern "C" int64_t idolq_q4_k_bytes(int64_t n, int64_t k) { return k > 0 && k % 256 == 0 && n >= 0 ? n * (k / 256) * 144 : 0; }
+
+extern "C" int idolq_q4_k_gemm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* w,
+                               int64_t n_total, int64_t n_offset, int64_t n, const void* bias, int bias_dtype,
+                               const void* residual, int residual_dtype, int64_t ldr, int act, int flags, void* y,
+                               int y_dtype, int64_t ldy, void* workspace, size_t workspace_bytes, void* stream) {
+    if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype) || (bias && !dtype_ok(bias_dtype)) ||
+        (residual && !dtype_ok(residual_dtype)))
+        return fail(IDOLQ_EINVAL, "unknown dtype code");
+    if (x_dtype == IDOLQ_F32) return fail(IDOLQ_EINVAL, "the Q4_K GEMM takes bf16 or fp16 activations");
+    if (m < 0 || n < 0 || k <= 0 || k % 256) return fail(IDOLQ_EINVAL, "need m >= 0, n >= 0 and k a positive multiple of 256");
+    if (n_offset < 0 || n_offset + n > n_total) return fail(IDOLQ_EINVAL, "column window outside the weight rows");
+    if (ldx < k || ldy < n || (residual && ldr < n)) return fail(IDOLQ_EINVAL, "row stride smaller than the row");
+    if (m > INT32_MAX / 2 || n_total > INT32_MAX / 2 || k > INT32_MAX / 2) return fail(IDOLQ_EINVAL, "dimension too large");
+    if (act < IDOLQ_ACT_NONE || act > IDOLQ_ACT_SILU) return fail(IDOLQ_EINVAL, "unknown activation");
+    if (flags & ~IDOLQ_FLAG_ROUND_BEFORE_BIAS) return fail(IDOLQ_EINVAL, "unknown flag for the Q4_K GEMM");
+    if (residual == y && residual && (residual_dtype != y_dtype || ldr != ldy))
+        return fail(IDOLQ_EINVAL, "a residual that aliases y must have y's dtype and stride");
+    const int64_t row_bytes = k / 256 * 144;
+    if (m * ldx * 2 >= (int64_t)UINT32_MAX || (n_total - n_offset) * row_bytes >= (int64_t)UINT32_MAX)
+        return fail(IDOLQ_EINVAL, "x or the weight window exceeds 2^32 elements / bytes");
+    if (m == 0 || n == 0) return IDOLQ_OK;
+    if (!x || !w || !y) return fail(IDOLQ_EINVAL, "x, w and y must be non-null");
+    const uint8_t* wwin = w + n_offset * row_bytes;
+    if ((reinterpret_cast<uintptr_t>(wwin) & 15) != 0) return fail(IDOLQ_EINVAL, "Q4_K weights must be 16-byte aligned");
+    if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || (ldx * 2) % 16 != 0)
+        return fail(IDOLQ_EINVAL, "the Q4_K GEMM needs 16-byte aligned activation rows");
+    GemmParams p{};
+    p.x = x;
+    p.ldx = ldx;
+    p.row_bytes = row_bytes;
+    p.w = wwin;
+    p.groups = (int)(n_total - n_offset);  // weight rows from p.w on
+    p.m = (int)m;
+    p.n = (int)n;
+    p.k = (int)k;
+    p.bias = bias ? static_cast<const char*>(bias) + n_offset * dtype_size(bias_dtype) : nullptr;
+    p.bias_dt = bias_dtype;
+    p.res = residual;
+    p.res_dt = residual_dtype;
+    p.ldr = ldr;
+    p.y = y;
+    p.y_dt = y_dtype;
+    p.ldy = ldy;
+    p.act = act;
+    p.flags = flags;
+    p.x_aligned = 1;
+    return launch_wide_any<true>(p, x_dtype == IDOLQ_BF16 ? XT_BF16 : XT_F16, workspace, workspace_bytes,
+                                 static_cast<hipStream_t>(stream));
+}

@@ -4,12 +4,12 @@ fused_linear keeps the reference's signature, validation and error messages (too
 numerics: weights dequantized to the activation dtype (the fp32 value, rounded), fp32 accumulation, the product
 rounded to the output dtype before the bias is added (tools/idol_triton.py:84-89). Per kind:
   Q8_0 (8)   libidolq's Q8_0 GEMM (idolq_q8_0_gemm, DEQUANT mode) on the GGUF blocks as they are;
-  Q4_0 (4)   the blocks re-encoded exactly as Q8_0 blocks (idolq_q4_0_to_q8_0: same scale, codes q - 8) into a
-             per-call scratch, then the same Q8_0 GEMM: the weights it multiplies are the reference's T(d * (q - 8));
-  Q4_K (44)  the matrix expanded to the activation dtype by libidolq (idolq_blocks_dequant, the reference's values)
-             into a per-call scratch, then a library GEMM (hipBLASLt through torch) with fp32 accumulation, rounded,
-             and the bias added in fp32 afterwards -- the reference's own route for its large products
-             (tools/idol_triton.py:112-117).
+  Q4_K (44)  libidolq's Q4_K GEMM (idolq_q4_k_gemm) on the GGUF super-blocks as they are: each weight is decoded to
+             T((d * sc) * q - dmin * m) inside the GEMM's weight loader, as the reference's kernel does
+             (tools/idol_triton.py:61-82); nothing is expanded or allocated besides the output;
+  Q4_0 (4)   the blocks as Q8_0 blocks with the same scale and codes q - 8 (exact), then the Q8_0 GEMM: the weights it
+             multiplies are the reference's T(d * (q - 8)). PackedLinear makes that copy once per device and passes
+             it as q8_blocks; a bare call re-encodes the blocks (idolq_q4_0_to_q8_0) first.
 """
 import torch
 
@@ -18,8 +18,9 @@ import idolq_lib as L
 KIND_Q4_0, KIND_Q8_0, KIND_Q4_K = 4, 8, 44
 
 
-def fused_linear(value, packed, shape, kind, bias=None):
-    """Multiply FP16/BF16 activations by Q4_0, Q8_0 or Q4_K weights on the GPU (tools/idol_triton.py:94-126)."""
+def fused_linear(value, packed, shape, kind, bias=None, *, q8_blocks=None):
+    """Multiply FP16/BF16 activations by Q4_0, Q8_0 or Q4_K weights on the GPU (tools/idol_triton.py:94-126).
+    q8_blocks: for kind 4, the Q8_0 re-encoding of `packed` (L.q4_0_to_q8_0) made beforehand."""
     if (not value.is_cuda or not packed.is_cuda or packed.dtype != torch.uint8
             or value.device != packed.device or value.dtype not in (torch.float16, torch.bfloat16)
             or len(shape) != 2 or value.shape[-1] != shape[1] or kind not in (KIND_Q4_0, KIND_Q8_0, KIND_Q4_K)):
@@ -39,15 +40,19 @@ def fused_linear(value, packed, shape, kind, bias=None):
     if not m:
         return torch.empty((*value.shape[:-1], n), device=value.device, dtype=value.dtype)
     w = packed.reshape(-1)
-    if kind == KIND_Q4_K:
-        dense = L.blocks_dequant(w, L.KIND_Q4_K, n, k, value.dtype)
-        out = torch.nn.functional.linear(x, dense)
-        if bias is not None:
-            out = (out.float() + bias.float()).to(value.dtype)
-        return out.reshape(*value.shape[:-1], n)
-    if kind == KIND_Q4_0:
-        w = L.q4_0_to_q8_0(w, n, k)
     # the bias enters the epilogue as fp32, as the reference loads it (an exact widening)
     b32 = bias.float() if bias is not None else None
+    if kind == KIND_Q4_K:
+        if x.data_ptr() % 16:  # the Q4_K kernel reads 16-byte aligned rows (k % 256 == 0): only a view can miss it
+            x = x.clone()
+        out = L.q4_k_gemm(x, w, n, bias=b32, flags=L.FLAG_ROUND_BEFORE_BIAS)
+        return out.reshape(*value.shape[:-1], n)
+    if kind == KIND_Q4_0:
+        if q8_blocks is not None:
+            if q8_blocks.numel() != n * (k // 32) * 34 or q8_blocks.device != value.device:
+                raise ValueError('invalid packed linear dimensions')
+            w = q8_blocks.reshape(-1)
+        else:
+            w = L.q4_0_to_q8_0(w, n, k)
     out = L.gemm(x, w, n, bias=b32, mode=L.MODE_DEQUANT, flags=L.FLAG_ROUND_BEFORE_BIAS)
     return out.reshape(*value.shape[:-1], n)

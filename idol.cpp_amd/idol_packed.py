@@ -36,6 +36,13 @@ class PackedLinear(torch.nn.Module):
         self.shape, self.kind, self.fused = shape, source.tensor_type, False
         self.register_buffer("packed", torch.from_numpy(np.array(source.data, dtype=np.uint8, copy=True).reshape(-1)))
         self.bias = None if bias is None else torch.nn.Parameter(bias.detach(), requires_grad=False)
+        self._q8_blocks = None  # Q4_0: its exact Q8_0 re-encoding on the packed buffer's device, made once
+
+    def _q4_0_as_q8_0(self):
+        if self._q8_blocks is None or self._q8_blocks.device != self.packed.device:
+            n, k = self.shape
+            self._q8_blocks = L.q4_0_to_q8_0(self.packed, n, k)
+        return self._q8_blocks
 
     def dequantize(self, dtype):
         """The dense (n, k) weight in `dtype` (tools/idol_packed.py:25-71)."""
@@ -63,7 +70,8 @@ class PackedLinear(torch.nn.Module):
 
     def forward(self, value):
         if self._fusable(value):
-            return fused_linear(value, self.packed, self.shape, _FUSED_KINDS[self.kind], self.bias)
+            q8 = self._q4_0_as_q8_0() if self.kind == GGMLQuantizationType.Q4_0 else None
+            return fused_linear(value, self.packed, self.shape, _FUSED_KINDS[self.kind], self.bias, q8_blocks=q8)
         return F.linear(value, self.dequantize(value.dtype), self.bias)
 
 

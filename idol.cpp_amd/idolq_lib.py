@@ -57,6 +57,9 @@ _SIGNATURES = {
     "idolq_to_gaussians": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "idolq_blocks_dequant": (_int, [_vp, _int, _i64, _i64, _vp, _int, _vp]),
     "idolq_q4_0_to_q8_0": (_int, [_vp, _i64, _i64, _vp, _vp]),
+    "idolq_q4_k_bytes": (_i64, [_i64, _i64]),
+    "idolq_q4_k_gemm": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _int, _vp, _int, _i64, _int,
+                               _int, _vp, _int, _i64, _vp, _sz, _vp]),
     "idolq_panel_bytes": (_i64, [_i64, _i64, _int, _int]),
     "idolq_panel_expand_f32": (_int, [_vp, _i64, _i64, _i64, _int, _int, _vp, _i64, _vp]),
     "idolq_panel_to_q8_0": (_int, [_vp, _i64, _i64, _i64, _int, _int, _vp, _vp, _vp]),
@@ -193,6 +196,34 @@ def gemm(x, w, n_total, n_offset=0, n=None, bias=None, residual=None, act=ACT_NO
                                _code(out), _row_stride(out), _ptr(workspace) if workspace is not None else None,
                                ws_bytes if workspace is not None else 0,
                                _stream(dev)))
+    return out
+
+
+def q4_k_gemm(x, w, n_total, n_offset=0, n=None, bias=None, residual=None, act=ACT_NONE, flags=0, out=None,
+              out_dtype=None, split=False):
+    """y = epilogue(x @ W[n_offset:n_offset+n]^T) with W GGUF Q4_K super-blocks, row-major, decoded inside the GEMM
+    (idolq_q4_k_gemm). x is bf16 or fp16 [m, k] with unit-stride rows; split=True passes the stream's DEQUANT
+    workspace (stream-K)."""
+    lib = load()
+    m, k = x.shape
+    if n is None:
+        n = n_total - n_offset
+    dev = _require_cuda(x, w, bias, residual, out)
+    if w.dtype != torch.uint8 or w.numel() != int(lib.idolq_q4_k_bytes(n_total, k)) or not w.is_contiguous():
+        raise ValueError("Q4_K weight size does not match its shape")
+    if bias is not None and (bias.dim() != 1 or bias.numel() != n_total or not bias.is_contiguous()):
+        raise ValueError("bias must be a contiguous vector of n_total values")
+    if out is None:
+        out = torch.empty((m, n), device=x.device, dtype=out_dtype or x.dtype)
+    ws = None
+    if split:
+        nbytes = int(lib.idolq_q8_0_gemm_workspace(m, k, MODE_DEQUANT))
+        ws = _split_workspace(x.device, nbytes)
+    ldr = _row_stride(residual) if residual is not None else 0
+    _check(lib.idolq_q4_k_gemm(_ptr(x), _code(x), m, k, _row_stride(x), _ptr(w), n_total, n_offset, n, _ptr(bias),
+                               _code(bias) if bias is not None else 0, _ptr(residual),
+                               _code(residual) if residual is not None else 0, ldr, act, flags, _ptr(out), _code(out),
+                               _row_stride(out), _ptr(ws), ws.numel() if ws is not None else 0, _stream(dev)))
     return out
 
 

@@ -205,6 +205,20 @@ int64_t idolq_blocks_bytes(int kind, int64_t n, int64_t k);
  * (PackedLinear.dequantize, tools/idol_packed.py:25-71), then rounded once. */
 int idolq_blocks_dequant(const uint8_t* w, int kind, int64_t n, int64_t k, void* out, int out_dtype, void* stream);
 
+/* Bytes of a row-major GGUF Q4_K matrix [n x k]: n * (k / 256) * 144 (0 when k % 256 != 0). */
+int64_t idolq_q4_k_bytes(int64_t n, int64_t k);
+
+/* y = epilogue(x * W^T) for GGUF Q4_K weights as they are stored (row-major 144-byte super-blocks of 256 values:
+ * fp16 d, fp16 dmin, 12 bytes of 6-bit scales and minimums, 128 bytes of 4-bit codes), decoded inside the GEMM's
+ * weight loader: each weight enters the MFMA as T((d * sc) * q - dmin * m), the reference's fused decode
+ * (tools/idol_triton.py:61-82), with fp32 accumulation (DEQUANT arithmetic). x bf16 or fp16 with 16-byte aligned rows,
+ * k % 256 == 0, the weight window 16-byte aligned; every other argument as idolq_q8_0_gemm (DEQUANT workspace optional,
+ * IDOLQ_FLAG_ROUND_BEFORE_BIAS for the fused path's bias order, tools/idol_triton.py:84-89). */
+int idolq_q4_k_gemm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* w, int64_t n_total,
+                    int64_t n_offset, int64_t n, const void* bias, int bias_dtype, const void* residual,
+                    int residual_dtype, int64_t ldr, int act, int flags, void* y, int y_dtype, int64_t ldy,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
 /* Re-encodes Q4_0 blocks [n x k] as Q8_0 blocks (same fp16 scale, codes q - 8): exact, so every Q8_0 GEMM mode
  * computes the Q4_0 layer's products (the Q4_0 case of tools/idol_triton.py:48-60). */
 int idolq_q4_0_to_q8_0(const uint8_t* w, int64_t n, int64_t k, uint8_t* out, void* stream);

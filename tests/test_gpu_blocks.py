@@ -86,3 +86,81 @@ def test_fused_q4_matches_reference_test(kind, code, rows, columns, width):
     # the expanded weights are the oracle's values
     want = O.blocks_values(data.reshape(-1), int(kind), columns, width)
     assert torch.equal(layer.dequantize(torch.float32).cpu(), torch.from_numpy(want))
+
+
+def q4k_blocks(n, k, seed, d=0.01, dmin=0.02):
+    """Random Q4_K super-blocks with finite scales (random 6-bit scales and minimums, random codes)."""
+    rng = np.random.default_rng(seed)
+    raw = rng.integers(0, 256, (n * (k // 256), 144), dtype=np.uint8)
+    raw[:, 0:2] = np.float16(rng.uniform(0.2, 1.0, raw.shape[0]) * d).view(np.uint8).reshape(-1, 2)
+    raw[:, 2:4] = np.float16(rng.uniform(0.2, 1.0, raw.shape[0]) * dmin).view(np.uint8).reshape(-1, 2)
+    return raw.reshape(-1)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_q4_k_gemm_decodes_every_weight_exactly(dtype):
+    # one-hot activation rows: y[i, j] = T(w[j, i]) exactly (a product by 1, sums of zeros), so the decode inside the
+    # GEMM's weight loader equals the expansion (and so the oracle) bit for bit at every position, for all 8 groups
+    n, k = 96, 512
+    raw = q4k_blocks(n, k, 31)
+    w = torch.from_numpy(raw).to(DEV)
+    x = torch.eye(k, device=DEV, dtype=dtype)
+    y = L.q4_k_gemm(x, w, n, out_dtype=torch.float32)
+    want = L.blocks_dequant(w, L.KIND_Q4_K, n, k, dtype).float().T
+    assert torch.equal(y, want)
+    assert torch.equal(want.T.cpu(), torch.from_numpy(O.blocks_values(raw, O.KIND_Q4_K, n, k)).to(dtype).float())
+
+
+@pytest.mark.parametrize("m,n_total,k,off,cnt,split", [(1, 7, 256, 0, 7, False), (300, 520, 1024, 0, 520, False),
+                                                         (513, 384, 2048, 96, 200, False), (4096, 1536, 1536, 0, 1536, True),
+                                                         (1024, 768, 6144, 0, 768, True), (128, 64, 256, 0, 64, False)])
+def test_q4_k_gemm_multiplies_the_decoded_weights(m, n_total, k, off, cnt, split):
+    # against an fp32 product of the expanded weights (the same products; fp32 sums in another order): 1e-5
+    print(f"q4_k gemm m={m} n={n_total} k={k} window {off}+{cnt} split={split}", flush=True)
+    raw = q4k_blocks(n_total, k, m + k)
+    w = torch.from_numpy(raw).to(DEV)
+    rng = np.random.default_rng(m)
+    x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(DEV).bfloat16()
+    b = torch.from_numpy(rng.normal(0, 0.1, n_total).astype(np.float32)).to(DEV)
+    y = L.q4_k_gemm(x, w, n_total, off, cnt, bias=b, out_dtype=torch.float32, split=split)
+    dense = L.blocks_dequant(w, L.KIND_Q4_K, n_total, k, torch.bfloat16).float()[off:off + cnt]
+    ref = x.float() @ dense.T + b[off:off + cnt]
+    assert norm_rel(y.cpu().numpy(), ref.cpu().numpy()) < 1e-5
+    again = L.q4_k_gemm(x, w, n_total, off, cnt, bias=b, out_dtype=torch.float32, split=split)
+    assert torch.equal(y, again)
+
+
+def test_q4_k_gemm_epilogue_and_fused_rounding():
+    # bias, residual aliasing y, tanh-GELU in the register epilogue (bf16 out) against the same steps in fp32 on the
+    # expanded weights; and the fused path's order: product rounded to bf16, then the bias
+    m, n, k = 512, 768, 1024
+    raw = q4k_blocks(n, k, 77)
+    w = torch.from_numpy(raw).to(DEV)
+    rng = np.random.default_rng(78)
+    x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(DEV).bfloat16()
+    b = torch.from_numpy(rng.normal(0, 0.1, n).astype(np.float32)).to(DEV)
+    res = torch.from_numpy(rng.standard_normal((m, n)).astype(np.float32)).to(DEV).bfloat16()
+    y = res.clone()
+    L.q4_k_gemm(x, w, n, bias=b, residual=y, act=L.ACT_GELU_TANH, out=y)
+    dense = L.blocks_dequant(w, L.KIND_Q4_K, n, k, torch.bfloat16).float()
+    v = x.float() @ dense.T + b + res.float()
+    ref = 0.5 * v * (1 + torch.tanh(0.7978845608028654 * (v + 0.044715 * v ** 3)))
+    assert norm_rel(y.float().cpu().numpy(), ref.bfloat16().float().cpu().numpy()) < 1e-3
+    plain = L.q4_k_gemm(x, w, n)
+    rounded = L.q4_k_gemm(x, w, n, bias=b, flags=L.FLAG_ROUND_BEFORE_BIAS)
+    assert torch.equal(rounded, (plain.float() + b).bfloat16())
+    with pytest.raises(ValueError):  # k = 320 is not a whole number of super-blocks
+        L.q4_k_gemm(x[:, :320], torch.zeros(n * 144, device=DEV, dtype=torch.uint8), n)
+
+
+def test_packed_q4_0_reencodes_once():
+    raw = random_blocks(O.KIND_Q4_0, 64, 256, 9)
+    layer = PackedLinear(SimpleNamespace(shape=np.array([256, 64]), tensor_type=T.Q4_0, data=raw), None).to(DEV)
+    enable_fused_packed(layer)
+    x = torch.randn(3, 256, device=DEV, dtype=torch.bfloat16)
+    with torch.no_grad():
+        a = layer(x)
+        cache = layer._q8_blocks
+        b = layer(x)
+    assert cache is not None and layer._q8_blocks is cache and torch.equal(a, b)
+    assert torch.equal(a, fused_linear(x, layer.packed, (64, 256), 4))
