@@ -334,8 +334,10 @@ __global__ __launch_bounds__(kWideThreads) void q8_wide_kernel(GemmParams p, Wid
                                           // consecutive rows over distinct banks)
     constexpr int ER = 32 * CH;           // rows per chunk
     constexpr int LPR = 8 * CT;           // read-back lanes per row
-    constexpr int RPI = 64 / LPR;         // rows per read-back instruction
+    constexpr int RPI = 64 / LPR;         // rows per read-back instruction (CT = 3: 2 rows of 24 lanes, lanes 48..63
+                                          // sit out: lane_ok)
     constexpr int NR = ER / RPI;          // read-back instructions per chunk
+    static_assert(ER % RPI == 0, "read-back rows");
     constexpr int NQ = RT / CH;           // chunks
     static_assert(4 * ER * EP * 4 <= C::Lds, "epilogue staging fits in LDS");
     // chunk q of the accumulators to the wave's staging rows; the reads that follow take values other lanes wrote:
@@ -366,7 +368,7 @@ __global__ __launch_bounds__(kWideThreads) void q8_wide_kernel(GemmParams p, Wid
         const int rl = lane / LPR, cl = lane % LPR;
         const int col = n0 + wave * 32 * CT + 4 * cl;
         // loads read clamped (valid) addresses, so only the stores carry bounds checks (n is a multiple of 4)
-        const bool col_ok = col < p.n;
+        const bool col_ok = col < p.n && lane < RPI * LPR;
         const int lcol = min(col, p.n - 4);
         const float4 b = p.bias ? *reinterpret_cast<const float4*>(static_cast<const float*>(p.bias) + lcol)
                                 : make_float4(0, 0, 0, 0);
@@ -422,7 +424,7 @@ __global__ __launch_bounds__(kWideThreads) void q8_wide_kernel(GemmParams p, Wid
 #pragma unroll 1
             for (int i = 0; i < NR * 4; ++i) {
                 const int lrow = RPI * (i >> 2) + rl, row = m0 + ER * q + lrow, cc = col + (i & 3);
-                if (row < p.m && cc < p.n) {
+                if (row < p.m && cc < p.n && lane < RPI * LPR) {
                     float x = st[lrow * EP + 4 * cl + (i & 3)];
                     if (round_first) x = round_through(p.y_dt, x);
                     if (p.bias) x += load_as_float(p.bias, p.bias_dt, cc);
@@ -574,36 +576,38 @@ __global__ __launch_bounds__(kWideThreads) void q8_wide_kernel(GemmParams p, Wid
                 if (finish) {
                     // every other part is stored: the tile's sum is part first + part first + 1 + ... + part last,
                     // added left to right whichever part finishes (this part's own sum enters at its range's
-                    // position), so the result does not depend on the order of arrival. Eight uint4 pieces of the
-                    // accumulators per batch: the running sum of a batch lives in t, the batch's loads in v.
+                    // position), so the result does not depend on the order of arrival. kB uint4 pieces of the
+                    // accumulators per batch (fewer for 256-row tiles, whose accumulators fill the AGPRs): the
+                    // running sum of a batch lives in t, the batch's loads in v.
+                    constexpr int kB = RT >= 8 ? 4 : 8;
                     auto slot_off = [&](int c) __attribute__((always_inline)) {
                         return (2 * c + (t0 > begin_of(c) ? 1 : 0)) * kSlot + tid * 16;
                     };
 #pragma unroll
-                    for (int q0 = 0; q0 < kQ; q0 += 8) {
-                        f32x4 t[8];
+                    for (int q0 = 0; q0 < kQ; q0 += kB) {
+                        f32x4 t[kB];
                         auto own = [&](int q) __attribute__((always_inline)) {
                             const f32x16& a = acc[((q0 + q) >> 2) / CT][((q0 + q) >> 2) % CT];
                             const int e0 = 4 * ((q0 + q) & 3);
                             return f32x4{a[e0], a[e0 + 1], a[e0 + 2], a[e0 + 3]};
                         };
                         for (int c = first; c <= last; ++c) {
-                            f32x4 v[8];
+                            f32x4 v[kB];
                             if (c == r) {
 #pragma unroll
-                                for (int q = 0; q < 8; ++q) v[q] = own(q);
+                                for (int q = 0; q < kB; ++q) v[q] = own(q);
                             } else {
                                 const int off = slot_off(c);
 #pragma unroll
-                                for (int q = 0; q < 8; ++q)
+                                for (int q = 0; q < kB; ++q)
                                     v[q] = __builtin_bit_cast(
                                         f32x4, __builtin_amdgcn_raw_buffer_load_b128(prs, off + (q0 + q) * 4096, 0, kCoherent));
                             }
 #pragma unroll
-                            for (int q = 0; q < 8; ++q) t[q] = c == first ? v[q] : t[q] + v[q];
+                            for (int q = 0; q < kB; ++q) t[q] = c == first ? v[q] : t[q] + v[q];
                         }
 #pragma unroll
-                        for (int q = 0; q < 8; ++q) {
+                        for (int q = 0; q < kB; ++q) {
                             f32x16& a = acc[((q0 + q) >> 2) / CT][((q0 + q) >> 2) % CT];
                             const int e0 = 4 * ((q0 + q) & 3);
 #pragma unroll
@@ -663,50 +667,79 @@ GemmParams column_window(GemmParams p, int n0, int n) {
     return p;
 }
 
-// Launch plans, costed in microseconds from MI355X measurements (4096 x 4096 outputs): a 64-deep stage of a round of
-// tiles takes 1.42 (256-row tiles) / 0.85 (128-row tiles); a tile's fixed part (first loads; the epilogue, where the
-// whole round's outputs are written at once, at the memory's write rate) 16 / 9.
-//   whole tiles, 256 or 128 rows;
-//   columns split in two launches: whole rounds of 256-row tiles on the first columns, 128-row tiles on the rest
-//     (fills the CUs when 256-row tiles would leave a partial round);
+// Launch plans, costed in microseconds from MI355X measurements: a 64-deep stage of a round of tiles takes STAGE, a
+// tile's fixed part (first loads; the epilogue, where the whole round's outputs are written at once, at the memory's
+// write rate) FIXED. Tiles: 256 x 256 (RT 8, CT 2) and 128 x 256 (4, 2). (128 x 384 tiles, which would make the MLP
+// block's and the denoiser's widths whole rounds, were measured 1.6x slower per stage: each dequantized weight
+// fragment then feeds 4 row tiles instead of 8, doubling the conversion work per MFMA.) Plans:
+//   whole tiles of one shape;
+//   columns split in two launches: whole rounds of 256-row tiles on the first columns, 128-row tiles on the rest;
 //   128-row tiles with stream-K over the tiles left after the whole rounds (a workspace is needed; about 6 more for
-//     the partial tiles). 256-row tiles are not split: their splits lose the L2 sharing of neighbouring workgroups.
+//     the partial tiles). 256-row tiles are not split: on the MLP block's down projection (4096 x 6144 -> 1536) their
+//     stream-K plan took 134 us against 105 us for 128-row stream-K; the split ranges lose the L2 sharing of
+//     neighbouring workgroups.
+struct WideShape {
+    int rt, ct;
+    double stage, fixed;
+};
+constexpr WideShape kShapes[2] = {{8, 2, 1.42, 16.0}, {4, 2, 0.85, 9.0}};
+constexpr int kNumShapes = sizeof(kShapes) / sizeof(kShapes[0]);
+
+template <typename T, bool Q4K, int RT, int CT>
+int launch_shape(GemmParams p, const WideSplit& sp, bool split, hipStream_t stream) {
+    return split ? launch_wide_s<T, RT, CT, true, Q4K>(p, sp, stream) : launch_wide_s<T, RT, CT, false, Q4K>(p, sp, stream);
+}
+
 template <typename T, bool Q4K>
 int launch_wide_dtype(GemmParams p, void* workspace, size_t workspace_bytes, hipStream_t stream) {
     const long cus = cu_count(), S = p.k / 64;
-    const long tm8 = (p.m + 255) / 256, tm4 = (p.m + 127) / 128, tn = (p.n + 255) / 256;
     auto rounds = [&](long tiles) { return (tiles + cus - 1) / cus; };
-    const double c8 = S * 1.42 + 16.0, c4 = S * 0.85 + 9.0;
-    const double whole8 = rounds(tm8 * tn) * c8, whole4 = rounds(tm4 * tn) * c4;
-    // split columns: as many column blocks as fill whole rounds of 256-row tiles, the rest with 128-row tiles
-    const long cb8 = (tm8 * tn) / cus * cus / tm8;  // column blocks of the first launch (whole rounds when tm8 divides)
-    const double hybrid = cb8 > 0 && cb8 < tn ? rounds(tm8 * cb8) * c8 + rounds(tm4 * (tn - cb8)) * c4 + 4.0 : -1.0;
-    const long dp4 = tm4 * tn / cus * cus, units = (tm4 * tn - dp4) * S;
-    const bool can_split = workspace && workspace_bytes >= kCountBytes + (size_t)2 * cus * 128 * 256 * 4 && units >= cus;
-    const double split4 = can_split ? (double)dp4 / cus * c4 + (double)rounds(units) * 0.85 + 2 * 9.0 + 6.0 : -1.0;
-
-    double best = whole8;
-    int plan = 0;
-    if (whole4 < best) best = whole4, plan = 1;
-    if (hybrid > 0 && hybrid < best) best = hybrid, plan = 2;
-    if (split4 > 0 && split4 < best) best = split4, plan = 3;
-    const WideSplit none{0, 0, 0, 0, nullptr, nullptr};
-    auto whole = [&](long tiles) { WideSplit sp = none; sp.G = (int)std::min(tiles, cus); return sp; };
-    switch (plan) {
-        case 0: return launch_wide_s<T, 8, 2, false, Q4K>(p, whole(tm8 * tn), stream);
-        case 1: return launch_wide_s<T, 4, 2, false, Q4K>(p, whole(tm4 * tn), stream);
-        case 2: {
-            const int n1 = (int)cb8 * 256;
-            int rc = launch_wide_s<T, 8, 2, false, Q4K>(column_window<Q4K>(p, 0, n1), whole(tm8 * cb8), stream);
-            if (rc) return rc;
-            return launch_wide_s<T, 4, 2, false, Q4K>(column_window<Q4K>(p, n1, p.n - n1), whole(tm4 * (tn - cb8)), stream);
-        }
-        default: {
-            WideSplit sp{(int)cus, (int)dp4, (int)(units / cus), (int)(units % cus),
-                         reinterpret_cast<float*>(static_cast<char*>(workspace) + kCountBytes), static_cast<int*>(workspace)};
-            return launch_wide_s<T, 4, 2, true, Q4K>(p, sp, stream);
+    auto tiles_of = [&](const WideShape& c) {
+        return (long)((p.m + 32 * c.rt - 1) / (32 * c.rt)) * ((p.n + 128 * c.ct - 1) / (128 * c.ct));
+    };
+    double best = -1.0;
+    int best_shape = 0;
+    bool best_split = false;
+    for (int i = 0; i < kNumShapes; ++i) {
+        const WideShape& c = kShapes[i];
+        const long tiles = tiles_of(c);
+        const double whole = rounds(tiles) * (S * c.stage + c.fixed);
+        if (best < 0 || whole < best) best = whole, best_shape = i, best_split = false;
+        if (c.rt == 4) {  // 256-row tiles are not split (below)
+            const long dp = tiles / cus * cus, units = (tiles - dp) * S;
+            const size_t need = kCountBytes + (size_t)2 * cus * (32 * c.rt) * (128 * c.ct) * 4;
+            if (workspace && workspace_bytes >= need && units >= cus) {
+                const double split = (double)dp / cus * (S * c.stage + c.fixed) + (double)rounds(units) * c.stage +
+                                     2 * c.fixed + 6.0;
+                if (split < best) best = split, best_shape = i, best_split = true;
+            }
         }
     }
+    // split columns: as many column blocks as fill whole rounds of 256-row tiles, the rest with 128-row tiles
+    const long tm8 = (p.m + 255) / 256, tm4 = (p.m + 127) / 128, tn = (p.n + 255) / 256;
+    const long cb8 = (tm8 * tn) / cus * cus / tm8;
+    const WideShape &c8 = kShapes[0], &c4 = kShapes[1];
+    const double hybrid = cb8 > 0 && cb8 < tn ? rounds(tm8 * cb8) * (S * c8.stage + c8.fixed) +
+                                                    rounds(tm4 * (tn - cb8)) * (S * c4.stage + c4.fixed) + 4.0
+                                              : -1.0;
+    const WideSplit none{0, 0, 0, 0, nullptr, nullptr};
+    auto whole = [&](long tiles) { WideSplit sp = none; sp.G = (int)std::min(tiles, cus); return sp; };
+    if (hybrid > 0 && hybrid < best) {
+        const int n1 = (int)cb8 * 256;
+        int rc = launch_wide_s<T, 8, 2, false, Q4K>(column_window<Q4K>(p, 0, n1), whole(tm8 * cb8), stream);
+        if (rc) return rc;
+        return launch_wide_s<T, 4, 2, false, Q4K>(column_window<Q4K>(p, n1, p.n - n1), whole(tm4 * (tn - cb8)), stream);
+    }
+    const WideShape& c = kShapes[best_shape];
+    const long tiles = tiles_of(c);
+    WideSplit sp = whole(tiles);
+    if (best_split) {
+        const long dp = tiles / cus * cus, units = (tiles - dp) * S;
+        sp = WideSplit{(int)cus, (int)dp, (int)(units / cus), (int)(units % cus),
+                       reinterpret_cast<float*>(static_cast<char*>(workspace) + kCountBytes), static_cast<int*>(workspace)};
+    }
+    if (best_shape == 0) return launch_wide_s<T, 8, 2, false, Q4K>(p, sp, stream);
+    return launch_shape<T, Q4K, 4, 2>(p, sp, best_split, stream);
 }
 
 }  // namespace
@@ -718,6 +751,7 @@ bool wide_eligible(const GemmParams& p, int xt, int mode) {
            (int64_t)p.groups * (p.k / 64) * kGroupBytes < (int64_t)UINT32_MAX;
 }
 
+// tile counters, then two partial tiles of the split shape (128 x 256 fp32) per CU
 size_t wide_workspace_bytes() { return kCountBytes + (size_t)2 * cu_count() * 128 * 256 * 4; }
 
 namespace {
