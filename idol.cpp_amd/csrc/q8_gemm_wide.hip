@@ -130,13 +130,13 @@ __device__ __forceinline__ uint2 q4k_dequant4(uint32_t nibbles, float a, float b
                       __builtin_bit_cast(uint32_t, __builtin_convertvector(hi * a - b, T2)));
 }
 
-template <typename T, int RT, int CT, int ACT, bool FAST, bool SPLIT, bool Q4K = false>
-__global__ __launch_bounds__(kWideThreads) void q8_wide_kernel(GemmParams p, WideSplit sp) {
+// The tiles of one launch shape (RT, CT), with this workgroup's share of them; smem: the kernel's LDS (C::Lds bytes).
+template <typename T, int RT, int CT, int ACT, bool FAST, bool SPLIT, bool Q4K>
+__device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit& sp, char* smem) {
     typedef WideCfg<RT, CT, Q4K> C;
     typedef typename PipeMfma<T>::vec Vec;
     typedef typename PipeMfma<T>::pair T2;
     constexpr int DA = C::DA, DW = C::DW;
-    __shared__ __attribute__((aligned(1024))) char smem[C::Lds];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -405,10 +405,13 @@ __global__ __launch_bounds__(kWideThreads) void q8_wide_kernel(GemmParams p, Wid
                 hi = hi + f32x2{b.z, b.w} + __builtin_convertvector(__builtin_bit_cast(T2, rr.y), f32x2);
                 lo = f32x2{act_fast<ACT>(lo.x), act_fast<ACT>(lo.y)};
                 hi = f32x2{act_fast<ACT>(hi.x), act_fast<ACT>(hi.y)};
-                if (col_ok && row < p.m)
-                    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.y) + (int64_t)row * p.ldy + col) =
-                        make_uint2(__builtin_bit_cast(uint32_t, __builtin_convertvector(lo, T2)),
-                                   __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, T2)));
+                // nontemporal: the round's outputs go out as they are stored instead of filling the L2 with dirty
+                // lines that the end of the kernel must write back (2-3% of the launch, measured)
+                if (col_ok && row < p.m) {
+                    uint32_t* dst = reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.y) + (int64_t)row * p.ldy + col);
+                    __builtin_nontemporal_store(__builtin_bit_cast(uint32_t, __builtin_convertvector(lo, T2)), dst);
+                    __builtin_nontemporal_store(__builtin_bit_cast(uint32_t, __builtin_convertvector(hi, T2)), dst + 1);
+                }
             }
             chunk_done();
         });
@@ -625,6 +628,24 @@ __global__ __launch_bounds__(kWideThreads) void q8_wide_kernel(GemmParams p, Wid
     }
 }
 
+template <typename T, int RT, int CT, int ACT, bool FAST, bool SPLIT, bool Q4K = false>
+__global__ __launch_bounds__(kWideThreads) void q8_wide_kernel(GemmParams p, WideSplit sp) {
+    __shared__ __attribute__((aligned(1024))) char smem[WideCfg<RT, CT, Q4K>::Lds];
+    wide_tiles<T, RT, CT, ACT, FAST, SPLIT, Q4K>(p, sp, smem);
+}
+
+// Two column ranges in one launch: 256 x 256 tiles on pa's columns, then 128 x 256 tiles on pb's (the column split
+// of the launch plans). A workgroup takes its share of the first and then of the second; the second range's first
+// loads follow the first range's epilogue without a kernel boundary between them.
+template <typename T, int ACT, bool FAST, bool Q4K>
+__global__ __launch_bounds__(kWideThreads) void q8_wide_pair_kernel(GemmParams pa, GemmParams pb) {
+    constexpr int kLds = WideCfg<8, 2, Q4K>::Lds > WideCfg<4, 2, Q4K>::Lds ? WideCfg<8, 2, Q4K>::Lds : WideCfg<4, 2, Q4K>::Lds;
+    __shared__ __attribute__((aligned(1024))) char smem[kLds];
+    const WideSplit whole{0, 0, 0, 0, nullptr, nullptr};
+    wide_tiles<T, 8, 2, ACT, FAST, false, Q4K>(pa, whole, smem);
+    wide_tiles<T, 4, 2, ACT, FAST, false, Q4K>(pb, whole, smem);
+}
+
 template <typename T, int RT, int CT, bool SPLIT, bool Q4K>
 int launch_wide_s(GemmParams p, const WideSplit& sp, hipStream_t stream) {
     const dim3 grid(sp.G), block(kWideThreads);
@@ -644,6 +665,29 @@ int launch_wide_s(GemmParams p, const WideSplit& sp, hipStream_t stream) {
     else
         hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, IDOLQ_ACT_NONE, true, SPLIT, Q4K>), grid, block, 0, stream, p, sp);
     return check_launch("q8_wide_kernel");
+}
+
+template <typename T, bool Q4K>
+int launch_wide_pair(GemmParams pa, GemmParams pb, int grid, hipStream_t stream) {
+    pa.tiles_m = (pa.m + 255) / 256;
+    pa.tiles_n = (pa.n + 255) / 256;
+    pb.tiles_m = (pb.m + 127) / 128;
+    pb.tiles_n = (pb.n + 255) / 256;
+    constexpr int kYdt = std::is_same<T, __bf16>::value ? IDOLQ_BF16 : IDOLQ_F16;
+    const GemmParams& p = pa;  // both ranges share dtypes, activation and alignment
+    const bool fast = p.y_vec4 && pa.n % 4 == 0 && pb.n % 4 == 0 && p.y_dt == kYdt && (!p.res || p.res_dt == kYdt) &&
+                      (!p.bias || p.bias_dt == IDOLQ_F32) &&
+                      (p.act == IDOLQ_ACT_NONE || p.act == IDOLQ_ACT_GELU_TANH || p.act == IDOLQ_ACT_RELU);
+    const dim3 g(grid), block(kWideThreads);
+    if (!fast)
+        hipLaunchKernelGGL((q8_wide_pair_kernel<T, IDOLQ_ACT_NONE, false, Q4K>), g, block, 0, stream, pa, pb);
+    else if (p.act == IDOLQ_ACT_GELU_TANH)
+        hipLaunchKernelGGL((q8_wide_pair_kernel<T, IDOLQ_ACT_GELU_TANH, true, Q4K>), g, block, 0, stream, pa, pb);
+    else if (p.act == IDOLQ_ACT_RELU)
+        hipLaunchKernelGGL((q8_wide_pair_kernel<T, IDOLQ_ACT_RELU, true, Q4K>), g, block, 0, stream, pa, pb);
+    else
+        hipLaunchKernelGGL((q8_wide_pair_kernel<T, IDOLQ_ACT_NONE, true, Q4K>), g, block, 0, stream, pa, pb);
+    return check_launch("q8_wide_pair_kernel");
 }
 
 // Workspace: tile counters in the first kCountBytes, then the partial tiles.
@@ -673,7 +717,8 @@ GemmParams column_window(GemmParams p, int n0, int n) {
 // block's and the denoiser's widths whole rounds, were measured 1.6x slower per stage: each dequantized weight
 // fragment then feeds 4 row tiles instead of 8, doubling the conversion work per MFMA.) Plans:
 //   whole tiles of one shape;
-//   columns split in two launches: whole rounds of 256-row tiles on the first columns, 128-row tiles on the rest;
+//   columns split in two ranges (one launch, q8_wide_pair_kernel): whole rounds of 256-row tiles on the first
+//     columns, 128-row tiles on the rest;
 //   128-row tiles with stream-K over the tiles left after the whole rounds (a workspace is needed; about 6 more for
 //     the partial tiles). 256-row tiles are not split: on the MLP block's down projection (4096 x 6144 -> 1536) their
 //     stream-K plan took 134 us against 105 us for 128-row stream-K; the split ranges lose the L2 sharing of
@@ -720,15 +765,14 @@ int launch_wide_dtype(GemmParams p, void* workspace, size_t workspace_bytes, hip
     const long cb8 = (tm8 * tn) / cus * cus / tm8;
     const WideShape &c8 = kShapes[0], &c4 = kShapes[1];
     const double hybrid = cb8 > 0 && cb8 < tn ? rounds(tm8 * cb8) * (S * c8.stage + c8.fixed) +
-                                                    rounds(tm4 * (tn - cb8)) * (S * c4.stage + c4.fixed) + 4.0
+                                                    rounds(tm4 * (tn - cb8)) * (S * c4.stage + c4.fixed)
                                               : -1.0;
     const WideSplit none{0, 0, 0, 0, nullptr, nullptr};
     auto whole = [&](long tiles) { WideSplit sp = none; sp.G = (int)std::min(tiles, cus); return sp; };
     if (hybrid > 0 && hybrid < best) {
         const int n1 = (int)cb8 * 256;
-        int rc = launch_wide_s<T, 8, 2, false, Q4K>(column_window<Q4K>(p, 0, n1), whole(tm8 * cb8), stream);
-        if (rc) return rc;
-        return launch_wide_s<T, 4, 2, false, Q4K>(column_window<Q4K>(p, n1, p.n - n1), whole(tm4 * (tn - cb8)), stream);
+        const long grid = std::min(std::max(tm8 * cb8, tm4 * (tn - cb8)), cus);
+        return launch_wide_pair<T, Q4K>(column_window<Q4K>(p, 0, n1), column_window<Q4K>(p, n1, p.n - n1), (int)grid, stream);
     }
     const WideShape& c = kShapes[best_shape];
     const long tiles = tiles_of(c);
