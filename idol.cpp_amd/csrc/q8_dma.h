@@ -11,6 +11,7 @@ typedef __attribute__((address_space(3))) char lds_char;
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
 
 template <typename T>
 struct PipeMfma;

@@ -119,17 +119,6 @@ __device__ __forceinline__ void q4k_header(uint4 hd, int pair, float (&ab)[4]) {
     }
 }
 
-// Four Q4_K codes (0..15, one per byte) to four operands T((d * sc) * q - dmin * m) = T(a * q - b); the product is
-// exact, so one rounding before the conversion, as the reference's expansion.
-template <typename T>
-__device__ __forceinline__ uint2 q4k_dequant4(uint32_t nibbles, float a, float b) {
-    typedef typename PipeMfma<T>::pair T2;
-    const f32x2 lo = {(float)(nibbles & 0xff), (float)((nibbles >> 8) & 0xff)};
-    const f32x2 hi = {(float)((nibbles >> 16) & 0xff), (float)(nibbles >> 24)};
-    return make_uint2(__builtin_bit_cast(uint32_t, __builtin_convertvector(lo * a - b, T2)),
-                      __builtin_bit_cast(uint32_t, __builtin_convertvector(hi * a - b, T2)));
-}
-
 // The tiles of one launch shape (RT, CT), with this workgroup's share of them; smem: the kernel's LDS (C::Lds bytes).
 template <typename T, int RT, int CT, int ACT, bool FAST, bool SPLIT, bool Q4K>
 __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit& sp, char* smem) {
@@ -251,30 +240,40 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
             }
         }
     };
-    // slice k < 2 CT of step j's weight operands: four codes (half k % 2 of group k / 2) to T(fp32(d) * q)
-    auto convert_slice = [&](int j, int set, int k) __attribute__((always_inline)) {
-        const int c = k >> 1, h = k & 1, b = j >> 1;
-        uint2 o;
+    // piece q < 4 CT of step j's weight operands: two codes to T(fp32(d) * q) (Q4K: T(a * q - b)), dword q % 4 of
+    // group q / 4's operand. Dwords 0, 1 come from the first code word of the step (x for even steps, z for odd
+    // ones), dwords 2, 3 from the second (y, w); each dword is the pair of codes at bytes 2 (q % 2), 2 (q % 2) + 1.
+    auto convert_piece = [&](int j, int set, int q) __attribute__((always_inline)) {
+        const int c = q >> 2, e = q & 3, b = j >> 1, sh = 16 * (e & 1);
+        uint32_t o;
         if constexpr (Q4K) {
             // step j: 32-group b = j / 2 of the pair (low nibbles for b = 0, high for b = 1), bytes of piece j % 2
-            const uint4 q = rc[c][0];
-            const uint32_t word = (j & 1) ? (h ? q.w : q.z) : (h ? q.y : q.x);
-            o = q4k_dequant4<T>(b ? (word >> 4) & 0x0f0f0f0fu : word & 0x0f0f0f0fu, rab[c][2 * b], rab[c][2 * b + 1]);
+            const uint4 w = rc[c][0];
+            const uint32_t word = (j & 1) ? ((e >> 1) ? w.w : w.z) : ((e >> 1) ? w.y : w.x);
+            const uint32_t nib = b ? (word >> 4) & 0x0f0f0f0fu : word & 0x0f0f0f0fu;
+            const f32x2 f = {(float)((nib >> sh) & 0xff), (float)((nib >> (sh + 8)) & 0xff)};
+            o = __builtin_bit_cast(uint32_t, __builtin_convertvector(f * rab[c][2 * b] - rab[c][2 * b + 1], T2));
         } else {
             const float d = half_bits_to_float((uint16_t)(rs[c] >> (16 * b)));
-            const uint4 q = rc[c][b];
-            o = dequant4<T>((j & 1) ? (h ? q.w : q.z) : (h ? q.y : q.x), d);
+            const uint4 w = rc[c][b];
+            const uint32_t word = (j & 1) ? ((e >> 1) ? w.w : w.z) : ((e >> 1) ? w.y : w.x);
+            const f32x2 f = {(float)(int)(int8_t)(uint8_t)(word >> sh), (float)(int)(int8_t)(uint8_t)(word >> (sh + 8))};
+            o = __builtin_bit_cast(uint32_t, __builtin_convertvector(f * d, T2));
         }
-        if (h) {
-            wq[set][c].z = o.x;
-            wq[set][c].w = o.y;
-        } else {
-            wq[set][c].x = o.x;
-            wq[set][c].y = o.y;
-        }
+        if (e == 0) wq[set][c].x = o;
+        else if (e == 1) wq[set][c].y = o;
+        else if (e == 2) wq[set][c].z = o;
+        else wq[set][c].w = o;
     };
     constexpr int NM = RT * CT;         // MFMAs per 16-deep step
-    constexpr int CV = NM - 2 * CT;     // first slot of the conversion slices
+    constexpr int NP = 4 * CT;          // conversion pieces per step
+    // The conversion (2.5 VALU instructions per code) is spread evenly over a step's MFMA slots, so that each slot's
+    // VALU work stays within the 32 cycles of its MFMA: in steps 0..2 piece q goes after MFMA PS q + PS - 1; in step 3,
+    // whose pieces convert the next stage's codes read from LDS in its first slots, the pieces fill the second half
+    // (FC on), PF per slot.
+    constexpr int PS = NM / NP;
+    constexpr int FC = NM / 2, PF = NP / (NM - FC);
+    static_assert(NM % NP == 0 && NP % (NM - FC) == 0, "conversion slots");
     // One 16-deep step: MFMA i on operand set `cur`, then slot(i) -- the other work of the stage (loads, the next
     // step's LDS reads and conversion) -- each slot pinned after its MFMA by a scheduling barrier, so that this work
     // is issued while the matrix core runs the step instead of being moved next to its first use.
@@ -294,15 +293,15 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
                 if (i < DW) issue_w_piece(ws, i);
             }
             if (i < RT) read_x1(buf, 1, 1, i);
-            if (i >= CV) convert_slice(1, 1, i - CV);
+            if (i % PS == PS - 1) convert_piece(1, 1, i / PS);
         });
         run_step(1, [&](int i) __attribute__((always_inline)) {
             if (i < RT) read_x1(buf, 2, 0, i);
-            if (i >= CV) convert_slice(2, 0, i - CV);
+            if (i % PS == PS - 1) convert_piece(2, 0, i / PS);
         });
         run_step(0, [&](int i) __attribute__((always_inline)) {
             if (i < RT) read_x1(buf, 3, 1, i);
-            if (i >= CV) convert_slice(3, 1, i - CV);
+            if (i % PS == PS - 1) convert_piece(3, 1, i / PS);
         });
     };
     // step 3 and the first operands of the next stage (buffers nb): its weight bytes, x operands and the conversion
@@ -316,7 +315,10 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
                 read_raw_piece(nb, i, next);
             else if (i <= CT + RT)
                 read_x1(nb, 0, 0, i - CT - 1);
-            if (i >= CV) convert_slice(0, 0, i - CV);
+            if (i >= FC) {
+#pragma unroll
+                for (int q = 0; q < PF; ++q) convert_piece(0, 0, (i - FC) * PF + q);
+            }
         });
     };
 
@@ -367,21 +369,35 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
         float* const st = reinterpret_cast<float*>(smem) + wave * ER * EP;
         const int rl = lane / LPR, cl = lane % LPR;
         const int col = n0 + wave * 32 * CT + 4 * cl;
-        // loads read clamped (valid) addresses, so only the stores carry bounds checks (n is a multiple of 4)
-        const bool col_ok = col < p.n && lane < RPI * LPR;
-        const int lcol = min(col, p.n - 4);
-        const float4 b = p.bias ? *reinterpret_cast<const float4*>(static_cast<const float*>(p.bias) + lcol)
-                                : make_float4(0, 0, 0, 0);
-        // the residual loads of the first PD chunks go out first, those of chunk q + PD before chunk q's stores (a
-        // wait for a load then never includes a store); PD = every chunk where the registers allow
+        // Every global access here is a buffer access whose offset is moved past the end of the buffer (kOff) when
+        // the element is outside y: such a load reads 0 and such a store is dropped. A missing bias or residual is a
+        // buffer of no bytes, so its loads read 0. The epilogue then has no branches around memory instructions,
+        // and the compiler's waits cover exactly the loads an instruction uses; around a branch they fall back to
+        // waiting for every earlier memory operation, the stores included, which serialized the output writes.
+        // The host keeps y and the residual below 2 GB for this path (byte offsets fit in 31 bits).
+        constexpr uint32_t kOff = 0x80000000u;
+        constexpr int kRaw = 0x00020000;  // raw buffer, 32-bit data format
+        const bool col_ok = (col < p.n) & (lane < RPI * LPR);
+        const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(p.y, 0, 0x7fffffff, kRaw);
+        const __amdgpu_buffer_rsrc_t rr =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.res ? p.res : p.y), 0, p.res ? 0x7fffffff : 0, kRaw);
+        const __amdgpu_buffer_rsrc_t rb =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.bias ? p.bias : p.y), 0, p.bias ? 0x7fffffff : 0, kRaw);
+        const f32x4 b = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, col_ok ? (uint32_t)col * 4 : kOff, 0, 0));
+        auto out_off = [&](int row, int64_t ld) __attribute__((always_inline)) {
+            const bool ok = col_ok & (row < p.m);  // no short-circuit: a select, not a branch
+            return ok ? (uint32_t)(row * (uint32_t)ld + col) * 2u : kOff;
+        };
+        // the residual loads of the first PD chunks go out first, those of chunk q + PD before chunk q's stores;
+        // PD = every chunk where the registers allow
         constexpr int PD = NQ * NR <= 32 ? NQ : 2;
         uint2 r2[PD][NR];
         auto load_res = [&](int q) __attribute__((always_inline)) {
 #pragma unroll
             for (int i = 0; i < NR; ++i) {
-                const int row = min(m0 + ER * q + RPI * i + rl, p.m - 1);
-                r2[q % PD][i] = p.res ? *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.res) + (int64_t)row * p.ldr + lcol)
-                                      : make_uint2(0, 0);
+                // (elements taken by index: a bit cast of an ext-vector element accessor (.y) read the wrong half)
+                const auto w = __builtin_amdgcn_raw_buffer_load_b64(rr, out_off(m0 + ER * q + RPI * i + rl, p.ldr), 0, 0);
+                r2[q % PD][i] = make_uint2(w[0], w[1]);
             }
         };
 #pragma unroll
@@ -400,18 +416,14 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
                     lo = __builtin_convertvector(__builtin_convertvector(lo, T2), f32x2);
                     hi = __builtin_convertvector(__builtin_convertvector(hi, T2), f32x2);
                 }
-                const uint2 rr = r2[q % PD][i];
-                lo = lo + f32x2{b.x, b.y} + __builtin_convertvector(__builtin_bit_cast(T2, rr.x), f32x2);
-                hi = hi + f32x2{b.z, b.w} + __builtin_convertvector(__builtin_bit_cast(T2, rr.y), f32x2);
+                const uint2 rr2 = r2[q % PD][i];
+                lo = lo + f32x2{b[0], b[1]} + __builtin_convertvector(__builtin_bit_cast(T2, rr2.x), f32x2);
+                hi = hi + f32x2{b[2], b[3]} + __builtin_convertvector(__builtin_bit_cast(T2, rr2.y), f32x2);
                 lo = f32x2{act_fast<ACT>(lo.x), act_fast<ACT>(lo.y)};
                 hi = f32x2{act_fast<ACT>(hi.x), act_fast<ACT>(hi.y)};
-                // nontemporal: the round's outputs go out as they are stored instead of filling the L2 with dirty
-                // lines that the end of the kernel must write back (2-3% of the launch, measured)
-                if (col_ok && row < p.m) {
-                    uint32_t* dst = reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.y) + (int64_t)row * p.ldy + col);
-                    __builtin_nontemporal_store(__builtin_bit_cast(uint32_t, __builtin_convertvector(lo, T2)), dst);
-                    __builtin_nontemporal_store(__builtin_bit_cast(uint32_t, __builtin_convertvector(hi, T2)), dst + 1);
-                }
+                const i32x2 o = {__builtin_bit_cast(int, __builtin_convertvector(lo, T2)),
+                                 __builtin_bit_cast(int, __builtin_convertvector(hi, T2))};
+                __builtin_amdgcn_raw_buffer_store_b64(o, ry, out_off(row, p.ldy), 0, 0);
             }
             chunk_done();
         });
@@ -475,7 +487,7 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) read_x1(0, 0, 0, rt);
 #pragma unroll
-        for (int k = 0; k < 2 * CT; ++k) convert_slice(0, 0, k);
+        for (int q = 0; q < NP; ++q) convert_piece(0, 0, q);
 
         const std::true_type issue;
         const std::false_type no_issue;
@@ -646,13 +658,19 @@ __global__ __launch_bounds__(kWideThreads) void q8_wide_pair_kernel(GemmParams p
     wide_tiles<T, 4, 2, ACT, FAST, false, Q4K>(pb, whole, smem);
 }
 
+// The register epilogue addresses y and the residual with 31-bit byte offsets (buffer accesses).
+bool below_2gb(const GemmParams& p) {
+    const int64_t y_end = ((int64_t)(p.m - 1) * p.ldy + p.n) * 2, r_end = ((int64_t)(p.m - 1) * p.ldr + p.n) * 2;
+    return y_end < INT32_MAX && (!p.res || r_end < INT32_MAX);
+}
+
 template <typename T, int RT, int CT, bool SPLIT, bool Q4K>
 int launch_wide_s(GemmParams p, const WideSplit& sp, hipStream_t stream) {
     const dim3 grid(sp.G), block(kWideThreads);
     p.tiles_m = (p.m + 32 * RT - 1) / (32 * RT);
     p.tiles_n = (p.n + 128 * CT - 1) / (128 * CT);
     constexpr int kYdt = std::is_same<T, __bf16>::value ? IDOLQ_BF16 : IDOLQ_F16;
-    const bool fast = p.y_vec4 && p.n % 4 == 0 && p.y_dt == kYdt && (!p.res || p.res_dt == kYdt) &&
+    const bool fast = p.y_vec4 && p.n % 4 == 0 && below_2gb(p) && p.y_dt == kYdt && (!p.res || p.res_dt == kYdt) &&
                       (!p.bias || p.bias_dt == IDOLQ_F32) &&
                       (p.act == IDOLQ_ACT_NONE || p.act == IDOLQ_ACT_GELU_TANH || p.act == IDOLQ_ACT_RELU);
     // the register epilogue's activation is a template argument; other activations take the general path
@@ -675,7 +693,8 @@ int launch_wide_pair(GemmParams pa, GemmParams pb, int grid, hipStream_t stream)
     pb.tiles_n = (pb.n + 255) / 256;
     constexpr int kYdt = std::is_same<T, __bf16>::value ? IDOLQ_BF16 : IDOLQ_F16;
     const GemmParams& p = pa;  // both ranges share dtypes, activation and alignment
-    const bool fast = p.y_vec4 && pa.n % 4 == 0 && pb.n % 4 == 0 && p.y_dt == kYdt && (!p.res || p.res_dt == kYdt) &&
+    const bool fast = p.y_vec4 && pa.n % 4 == 0 && pb.n % 4 == 0 && below_2gb(pa) && below_2gb(pb) && p.y_dt == kYdt &&
+                      (!p.res || p.res_dt == kYdt) &&
                       (!p.bias || p.bias_dt == IDOLQ_F32) &&
                       (p.act == IDOLQ_ACT_NONE || p.act == IDOLQ_ACT_GELU_TANH || p.act == IDOLQ_ACT_RELU);
     const dim3 g(grid), block(kWideThreads);
