@@ -64,10 +64,14 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 
 template <typename T>
-__global__ __launch_bounds__(256) void attn_mfma_hd64(AttnParams p) {
+__global__ __launch_bounds__(256, 3) void attn_mfma_hd64(AttnParams p) {
     typedef typename AttnMfma<T>::vec Vec;
-    __shared__ __attribute__((aligned(16))) uint16_t k_lds[kBKV * kKPitch];
-    __shared__ __attribute__((aligned(16))) uint16_t vt_lds[kHD * kVPitch];
+    // two key/value tiles in LDS: tile j is read from buffer j % 2 while tile j + 1 is loaded into registers and then
+    // written to the other buffer; one barrier per tile publishes the next tile
+    __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][kBKV * kKPitch];
+    __shared__ __attribute__((aligned(16))) uint16_t vt_lds[2][kHD * kVPitch];
+    __shared__ uint32_t vote[2][4];
+    __shared__ uint32_t vexp_vote[4];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t b = blockIdx.z, h = blockIdx.y;
@@ -76,8 +80,13 @@ __global__ __launch_bounds__(256) void attn_mfma_hd64(AttnParams p) {
     const int half = lane >> 5;
 
     const uint16_t* qbase = static_cast<const uint16_t*>(p.q) + b * p.q_bs + h * kHD;
-    const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + b * p.kv_bs + h * kHD;
-    const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + b * p.kv_bs + h * kHD;
+    // K and V rows through buffer loads: keys past lk get an offset past the buffer and read 0 (no branch around the
+    // loads); the host keeps lk * ldkv elements below 2^30
+    constexpr uint32_t kOff = 0x80000000u;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(static_cast<const uint16_t*>(p.k) + b * p.kv_bs + h * kHD), 0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(static_cast<const uint16_t*>(p.v) + b * p.kv_bs + h * kHD), 0, 0x7fffffff, 0x00020000);
 
     // Q^T operand: lane supplies query qi, d = 16 c + 8 half + e.
     Vec qf[4];
@@ -107,85 +116,87 @@ __global__ __launch_bounds__(256) void attn_mfma_hd64(AttnParams p) {
     // power of two that brings its largest magnitude below 2^15, and its P * V is added as 2^e (2^-e o + P V')
     // (exact scalings); other tiles, and every fp16 input, take the plain fp16 V^T.
     constexpr bool kWideV = std::is_same<T, __bf16>::value;
-    __shared__ uint32_t vote[4];
 
-    // one 64-key tile; MASK: the last tile, which holds fewer than 64 keys; FIRST: the first tile, which sets mc
-    auto tile = [&](int64_t j0, auto mask_tag, auto first_tag) __attribute__((always_inline)) {
-        constexpr bool MASK = decltype(mask_tag)::value, FIRST = decltype(first_tag)::value;
-        __syncthreads();
-        // Stage K [key][d] and V^T [d][key] (fp16): thread t takes keys 2 (t / 8) and 2 (t / 8) + 1, d chunk
-        // 8 (t % 8); V^T gets one (key, key + 1) pair per d and dword store.
-        const int kp = threadIdx.x >> 3, part = threadIdx.x & 7;
-        uint32_t v0[4], v1[4];
-        bool big = false;
-        {
-            uint4 kr[2], vr[2];
+    // staging: thread t takes keys 2 (t / 8) and 2 (t / 8) + 1, d chunk 8 (t % 8); V^T gets one (key, key + 1) pair
+    // per d and dword store
+    const int kp = threadIdx.x >> 3, part = threadIdx.x & 7;
+    uint4 kr[2], vr[2];
+    auto load_tile = [&](int64_t j0) __attribute__((always_inline)) {
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int64_t key = j0 + 2 * kp + i;
-                kr[i] = make_uint4(0, 0, 0, 0);
-                vr[i] = make_uint4(0, 0, 0, 0);
-                if (key < p.lk) {
-                    kr[i] = *reinterpret_cast<const uint4*>(kbase + key * p.ldkv + 8 * part);
-                    vr[i] = *reinterpret_cast<const uint4*>(vbase + key * p.ldkv + 8 * part);
-                }
-                *reinterpret_cast<uint4*>(k_lds + (2 * kp + i) * kKPitch + 8 * part) = kr[i];
-            }
-            v0[0] = vr[0].x, v0[1] = vr[0].y, v0[2] = vr[0].z, v0[3] = vr[0].w;
-            v1[0] = vr[1].x, v1[1] = vr[1].y, v1[2] = vr[1].z, v1[3] = vr[1].w;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint16_t b0 = (uint16_t)(v0[e >> 1] >> (16 * (e & 1))), b1 = (uint16_t)(v1[e >> 1] >> (16 * (e & 1)));
-                f16x2 pair;
-                if constexpr (!kWideV) {
-                    pair = f16x2{__builtin_bit_cast(_Float16, b0), __builtin_bit_cast(_Float16, b1)};
-                } else {
-                    const f32x2 f = {bf16_bits_to_float(b0), bf16_bits_to_float(b1)};
-                    big = big || fabsf(f.x) >= 65504.0f || fabsf(f.y) >= 65504.0f;
-                    pair = __builtin_convertvector(f, f16x2);
-                }
-                *reinterpret_cast<f16x2*>(vt_lds + (8 * part + e) * kVPitch + 2 * kp) = pair;
-            }
+        for (int i = 0; i < 2; ++i) {
+            const int64_t key = j0 + 2 * kp + i;
+            const uint32_t off = key < p.lk ? (uint32_t)(key * p.ldkv + 8 * part) * 2u : kOff;
+            kr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+            vr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
         }
-        int vexp = 0;  // this tile's V^T holds fp16(v * 2^-vexp)
+    };
+    // the V values of thread-local element e of key kp2 + i (16-bit bits)
+    auto vbits = [&](int i, int e) __attribute__((always_inline)) {
+        const uint32_t word = (e >> 1) == 0 ? vr[i].x : (e >> 1) == 1 ? vr[i].y : (e >> 1) == 2 ? vr[i].z : vr[i].w;
+        return (uint16_t)(word >> (16 * (e & 1)));
+    };
+    // registers -> LDS buffer buf; with kWideV, records whether any staged |v| >= 65504 (one vote per wave)
+    auto stage_tile = [&](int buf) __attribute__((always_inline)) {
+        bool big = false;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) *reinterpret_cast<uint4*>(&k_lds[buf][(2 * kp + i) * kKPitch + 8 * part]) = kr[i];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint16_t b0 = vbits(0, e), b1 = vbits(1, e);
+            f16x2 pair;
+            if constexpr (!kWideV) {
+                pair = f16x2{__builtin_bit_cast(_Float16, b0), __builtin_bit_cast(_Float16, b1)};
+            } else {
+                const f32x2 f = {bf16_bits_to_float(b0), bf16_bits_to_float(b1)};
+                big = big || fabsf(f.x) >= 65504.0f || fabsf(f.y) >= 65504.0f;
+                pair = __builtin_convertvector(f, f16x2);
+            }
+            *reinterpret_cast<f16x2*>(&vt_lds[buf][(8 * part + e) * kVPitch + 2 * kp]) = pair;
+        }
         if constexpr (kWideV) {
             const uint32_t wave_big = __builtin_amdgcn_ballot_w64(big) != 0 ? 1u : 0u;  // every lane takes part
-            if (lane == 0) vote[wave] = wave_big;
-            __syncthreads();
-            if ((vote[0] | vote[1] | vote[2] | vote[3]) != 0) {  // workgroup-uniform; rare
-                // the largest exponent field among the tile's values (bf16 bits 14..7)
-                uint32_t eb = 0;
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    eb = max(eb, max(max(v0[e] & 0x7f80u, (v0[e] >> 16) & 0x7f80u), max(v1[e] & 0x7f80u, (v1[e] >> 16) & 0x7f80u)));
-#pragma unroll
-                for (int off = 32; off > 0; off >>= 1) eb = max(eb, (uint32_t)__shfl_xor((int)eb, off));
-                __syncthreads();  // every wave has read the vote
-                if (lane == 0) vote[wave] = eb;
-                __syncthreads();
-                eb = max(max(vote[0], vote[1]), max(vote[2], vote[3]));
-                // |v| < 2^(E + 1), E = (eb >> 7) - 127 >= 15: scaled by 2^-(E - 14) every value is below 2^15
-                vexp = (int)(eb >> 7) - 127 - 14;
-                const float down = __builtin_bit_cast(float, (uint32_t)(127 - vexp) << 23);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const uint16_t b0 = (uint16_t)(v0[e >> 1] >> (16 * (e & 1))), b1 = (uint16_t)(v1[e >> 1] >> (16 * (e & 1)));
-                    const f32x2 f = {bf16_bits_to_float(b0) * down, bf16_bits_to_float(b1) * down};
-                    *reinterpret_cast<f16x2*>(vt_lds + (8 * part + e) * kVPitch + 2 * kp) = __builtin_convertvector(f, f16x2);
-                }
-                __syncthreads();
-            }
-        } else {
-            __syncthreads();
+            if (lane == 0) vote[buf][wave] = wave_big;
         }
+    };
+    // the rare path for tile buf (after the barrier that published it, while vr still holds its values): every wave
+    // saw the same votes, so the whole workgroup re-stages its V^T scaled by 2^-vexp; returns vexp
+    auto rescale_tile = [&](int buf) __attribute__((always_inline)) {
+        // the largest exponent field among the tile's values (bf16 bits 14..7)
+        uint32_t eb = 0;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t w4[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) eb = max(eb, max(w4[e] & 0x7f80u, (w4[e] >> 16) & 0x7f80u));
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) eb = max(eb, (uint32_t)__shfl_xor((int)eb, off));
+        if (lane == 0) vexp_vote[wave] = eb;
+        __syncthreads();
+        eb = max(max(vexp_vote[0], vexp_vote[1]), max(vexp_vote[2], vexp_vote[3]));
+        // |v| < 2^(E + 1), E = (eb >> 7) - 127 >= 15: scaled by 2^-(E - 14) every value is below 2^15
+        const int vexp = (int)(eb >> 7) - 127 - 14;
+        const float down = __builtin_bit_cast(float, (uint32_t)(127 - vexp) << 23);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const f32x2 f = {bf16_bits_to_float(vbits(0, e)) * down, bf16_bits_to_float(vbits(1, e)) * down};
+            *reinterpret_cast<f16x2*>(&vt_lds[buf][(8 * part + e) * kVPitch + 2 * kp]) = __builtin_convertvector(f, f16x2);
+        }
+        __syncthreads();  // the scaled V^T is in place; every wave has read vexp_vote
+        return vexp;
+    };
 
+    // the scores, softmax and P * V of the tile in buffer buf (keys j0 ..); MASK: the last tile, which holds fewer
+    // than 64 keys; FIRST: the first tile, which sets mc
+    auto compute = [&](int buf, int64_t j0, int vexp, auto mask_tag, auto first_tag) __attribute__((always_inline)) {
+        constexpr bool MASK = decltype(mask_tag)::value, FIRST = decltype(first_tag)::value;
         // S^T for 64 keys: two 32-key sub-tiles, 4 MFMAs each over d.
         f32x16 s[2];
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
 #pragma unroll
             for (int c4 = 0; c4 < 4; ++c4) {
-                const Vec a = *reinterpret_cast<const Vec*>(k_lds + (st * 32 + (lane & 31)) * kKPitch + 16 * c4 + 8 * half);
+                const Vec a = *reinterpret_cast<const Vec*>(&k_lds[buf][(st * 32 + (lane & 31)) * kKPitch + 16 * c4 + 8 * half]);
                 s[st] = AttnMfma<T>::run(a, qf[c4], c4 == 0 ? f32x16{} : s[st]);
             }
         }
@@ -245,18 +256,18 @@ __global__ __launch_bounds__(256) void attn_mfma_hd64(AttnParams p) {
                 for (int e = 0; e < 8; e += 2) {
                     const f32x2 pe = {__builtin_amdgcn_exp2f(s[st][8 * kc + e]),
                                       __builtin_amdgcn_exp2f(s[st][8 * kc + e + 1])};
-                    const f16x2 h = __builtin_convertvector(pe, f16x2);
-                    pf[e] = h.x;
-                    pf[e + 1] = h.y;
+                    const f16x2 hp = __builtin_convertvector(pe, f16x2);
+                    pf[e] = hp.x;
+                    pf[e + 1] = hp.y;
                     // the normalizer sums the probabilities as rounded for the product
-                    l_part = __builtin_amdgcn_fdot2(h, ones, l_part, false);
+                    l_part = __builtin_amdgcn_fdot2(hp, ones, l_part, false);
                 }
                 const int key0 = st * 32 + 16 * kc + 4 * half;
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
                     const int d = t * 32 + (lane & 31);
-                    const uint2 lo = *reinterpret_cast<const uint2*>(vt_lds + d * kVPitch + key0);
-                    const uint2 hi = *reinterpret_cast<const uint2*>(vt_lds + d * kVPitch + key0 + 8);
+                    const uint2 lo = *reinterpret_cast<const uint2*>(&vt_lds[buf][d * kVPitch + key0]);
+                    const uint2 hi = *reinterpret_cast<const uint2*>(&vt_lds[buf][d * kVPitch + key0 + 8]);
                     const f16x8 va = __builtin_bit_cast(f16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
                     o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pf, o[t], 0, 0, 0);
                 }
@@ -269,13 +280,32 @@ __global__ __launch_bounds__(256) void attn_mfma_hd64(AttnParams p) {
                 for (int r = 0; r < 16; ++r) o[t][r] *= up;
         }
     };
+    // tile j0 (in buffer buf): the rare rescaling, the next tile's loads, the product, the next tile's staging and
+    // the barrier that publishes it
+    auto step = [&](int buf, int64_t j0, bool has_next, auto mask_tag, auto first_tag) __attribute__((always_inline)) {
+        int vexp = 0;
+        if constexpr (kWideV) {
+            if ((vote[buf][0] | vote[buf][1] | vote[buf][2] | vote[buf][3]) != 0) vexp = rescale_tile(buf);  // uniform
+        }
+        if (has_next) load_tile(j0 + kBKV);
+        compute(buf, j0, vexp, mask_tag, first_tag);
+        if (has_next) stage_tile(buf ^ 1);
+        __syncthreads();
+    };
+
+    load_tile(0);
+    stage_tile(0);
+    __syncthreads();
     const int64_t full_end = p.lk / kBKV * kBKV;
     if (full_end == 0) {
-        tile(0, std::true_type{}, std::true_type{});
+        step(0, 0, false, std::true_type{}, std::true_type{});
     } else {
-        tile(0, std::false_type{}, std::true_type{});
-        for (int64_t j0 = kBKV; j0 < full_end; j0 += kBKV) tile(j0, std::false_type{}, std::false_type{});
-        if (full_end < p.lk) tile(full_end, std::true_type{}, std::false_type{});
+        const bool tail = full_end < p.lk;
+        step(0, 0, kBKV < p.lk, std::false_type{}, std::true_type{});
+        int buf = 1;
+        for (int64_t j0 = kBKV; j0 < full_end; j0 += kBKV, buf ^= 1)
+            step(buf, j0, j0 + kBKV < p.lk, std::false_type{}, std::false_type{});
+        if (tail) step(buf, full_end, false, std::true_type{}, std::false_type{});
     }
 
     const float l_run = l_part + __shfl_xor(l_part, 32);
@@ -516,7 +546,7 @@ extern "C" int idolq_attention(const void* q, const void* k, const void* v, int 
     const bool aligned = reinterpret_cast<uintptr_t>(q) % 16 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
                          reinterpret_cast<uintptr_t>(v) % 16 == 0 && (ldq * esz) % 16 == 0 &&
                          (ldkv * esz) % 16 == 0 && (q_bs * esz) % 16 == 0 && (kv_bs * esz) % 16 == 0;
-    if (dtype != IDOLQ_F32 && head_dim == kHD && aligned) {
+    if (dtype != IDOLQ_F32 && head_dim == kHD && aligned && lk * ldkv < ((int64_t)1 << 30)) {
         const dim3 grid((unsigned)((lq + kBQ - 1) / kBQ), (unsigned)heads, (unsigned)batch);
         if (dtype == IDOLQ_BF16)
             hipLaunchKernelGGL(attn_mfma_hd64<__bf16>, grid, dim3(256), 0, s, p);
