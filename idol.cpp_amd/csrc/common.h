@@ -111,10 +111,10 @@ __device__ __forceinline__ float apply_act(int act, float v) {
         case IDOLQ_ACT_GELU_ERF: return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
         case IDOLQ_ACT_GELU_TANH: {
             // 0.5 v (1 + tanh(u)) = v / (1 + exp(-2u)), u = sqrt(2/pi) (v + 0.044715 v^3): one exp2 and one
-            // reciprocal (a few ulp, far below the 16-bit output rounding); exp2 -> inf gives -0 for large negative v
-            const float u2 = v * fmaf(0.0713548162726f, v * v, 1.5957691216057308f);  // 2u
-            const float e = __builtin_amdgcn_exp2f(-1.4426950408889634f * u2);
-            return v * __builtin_amdgcn_rcpf(1.0f + e);
+            // reciprocal (a few ulp, far below the 16-bit output rounding); exp2 -> inf gives -0 for large negative v.
+            // The exponent -2u log2(e) = v (-0.10294324 v^2 - 2.3022082): 2 sqrt(2/pi) (1, 0.044715) times -log2(e).
+            const float t = v * fmaf(-1.0294324160e-01f, v * v, -2.3022081852e+00f);
+            return v * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
         }
         case IDOLQ_ACT_RELU: return v > 0.0f ? v : 0.0f;
         case IDOLQ_ACT_SILU: return v / (1.0f + expf(-v));

@@ -591,42 +591,55 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
                 if (finish) {
                     // every other part is stored: the tile's sum is part first + part first + 1 + ... + part last,
                     // added left to right whichever part finishes (this part's own sum enters at its range's
-                    // position), so the result does not depend on the order of arrival. kB uint4 pieces of the
-                    // accumulators per batch (fewer for 256-row tiles, whose accumulators fill the AGPRs): the
-                    // running sum of a batch lives in t, the batch's loads in v.
-                    constexpr int kB = RT >= 8 ? 4 : 8;
+                    // position), so the result does not depend on the order of arrival. The accumulators are taken
+                    // in kH passes of kP uint4 pieces (register budget); in a pass every stored part is read with
+                    // one batch of loads (one round trip per part): the parts before this one are summed into t,
+                    // then this part's own pieces are added to t, then the parts after it.
+                    constexpr int kH = RT >= 8 ? 4 : 2, kP = kQ / kH;
                     auto slot_off = [&](int c) __attribute__((always_inline)) {
                         return (2 * c + (t0 > begin_of(c) ? 1 : 0)) * kSlot + tid * 16;
                     };
 #pragma unroll
-                    for (int q0 = 0; q0 < kQ; q0 += kB) {
-                        f32x4 t[kB];
-                        auto own = [&](int q) __attribute__((always_inline)) {
-                            const f32x16& a = acc[((q0 + q) >> 2) / CT][((q0 + q) >> 2) % CT];
-                            const int e0 = 4 * ((q0 + q) & 3);
-                            return f32x4{a[e0], a[e0 + 1], a[e0 + 2], a[e0 + 3]};
+                    for (int hp = 0; hp < kH; ++hp) {
+                        auto piece = [&](int q) __attribute__((always_inline)) -> f32x16& {
+                            return acc[((hp * kP + q) >> 2) / CT][((hp * kP + q) >> 2) % CT];
                         };
-                        for (int c = first; c <= last; ++c) {
-                            f32x4 v[kB];
-                            if (c == r) {
+                        auto load_part = [&](int c, f32x4 (&v)[kP]) __attribute__((always_inline)) {
+                            const int off = slot_off(c);
 #pragma unroll
-                                for (int q = 0; q < kB; ++q) v[q] = own(q);
-                            } else {
-                                const int off = slot_off(c);
+                            for (int q = 0; q < kP; ++q)
+                                v[q] = __builtin_bit_cast(
+                                    f32x4, __builtin_amdgcn_raw_buffer_load_b128(prs, off + (hp * kP + q) * 4096, 0, kCoherent));
+                        };
+                        f32x4 t[kP];
+                        if (first < r) {
+                            load_part(first, t);
+                            for (int c = first + 1; c < r; ++c) {
+                                f32x4 v[kP];
+                                load_part(c, v);
 #pragma unroll
-                                for (int q = 0; q < kB; ++q)
-                                    v[q] = __builtin_bit_cast(
-                                        f32x4, __builtin_amdgcn_raw_buffer_load_b128(prs, off + (q0 + q) * 4096, 0, kCoherent));
+                                for (int q = 0; q < kP; ++q) t[q] = t[q] + v[q];
                             }
 #pragma unroll
-                            for (int q = 0; q < kB; ++q) t[q] = c == first ? v[q] : t[q] + v[q];
+                            for (int q = 0; q < kP; ++q) {
+                                f32x16& a = piece(q);
+                                const int e0 = 4 * ((hp * kP + q) & 3);
+                                const f32x4 own = {a[e0], a[e0 + 1], a[e0 + 2], a[e0 + 3]};
+                                const f32x4 sum = t[q] + own;
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) a[e0 + e] = sum[e];
+                            }
                         }
+                        for (int c = r + 1; c <= last; ++c) {
+                            f32x4 v[kP];
+                            load_part(c, v);
 #pragma unroll
-                        for (int q = 0; q < kB; ++q) {
-                            f32x16& a = acc[((q0 + q) >> 2) / CT][((q0 + q) >> 2) % CT];
-                            const int e0 = 4 * ((q0 + q) & 3);
+                            for (int q = 0; q < kP; ++q) {
+                                f32x16& a = piece(q);
+                                const int e0 = 4 * ((hp * kP + q) & 3);
 #pragma unroll
-                            for (int e = 0; e < 4; ++e) a[e0 + e] = t[q][e];
+                                for (int e = 0; e < 4; ++e) a[e0 + e] = a[e0 + e] + v[q][e];
+                            }
                         }
                     }
                     if (tid == 0) __hip_atomic_store(sp.count + first, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
