@@ -50,7 +50,7 @@ def parse():
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
-    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--warmup", type=int, default=30)
     p.add_argument("--mode", choices=["dequant", "exact", "int8"], default="dequant",
                    help="GEMM arithmetic: bf16-dequant MFMA (the reference GPU path's numerics), exact-code bf16 "
                         "MFMA with per-block fp32 scaling, or int8 MFMA on quantized activations")
@@ -189,31 +189,32 @@ def run_gpu(args):
     inputs = mlp_inputs(torch, L)
     blk = MlpBlock(torch, L, mode, inputs)
 
-    def step(events=None):
-        if events is not None:
-            events[0].record()
+    def step(before_up=None, before_down=None):
+        if before_up is not None:
+            before_up.record()
         blk.up()
-        if events is not None:
-            events[1].record()
+        if before_down is not None:
+            before_down.record()
         blk.down()
-        if events is not None:
-            events[2].record()
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    # Events on the stream the kernels are launched on (torch's current stream, which idolq_lib passes down).
+    # Events on the stream the kernels are launched on (torch's current stream, which idolq_lib passes down): one
+    # before each up launch, one before each down launch and one after the last step, so that step i's up GEMM is
+    # ev[2 i] -> ev[2 i + 1] and its down GEMM ev[2 i + 1] -> ev[2 i + 2] (two markers per step in the queue).
     stream = torch.cuda.current_stream()
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(2 * args.steps + 1)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     with torch.cuda.stream(stream):
         for i in range(args.steps):
-            step(evs[i])
+            step(evs[2 * i], evs[2 * i + 1])
+        evs[-1].record()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    up_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
-    down_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
+    up_ms = sum(evs[2 * i].elapsed_time(evs[2 * i + 1]) for i in range(args.steps)) / args.steps
+    down_ms = sum(evs[2 * i + 1].elapsed_time(evs[2 * i + 2]) for i in range(args.steps)) / args.steps
     flop_gemm = 2.0 * M * D * H
     ms_per_step = elapsed * 1e3 / args.steps
     value = 2 * flop_gemm / (ms_per_step * 1e-3) / 1e12
