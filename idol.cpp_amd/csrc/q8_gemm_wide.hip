@@ -120,7 +120,8 @@ __device__ __forceinline__ void q4k_header(uint4 hd, int pair, float (&ab)[4]) {
 }
 
 // The tiles of one launch shape (RT, CT), with this workgroup's share of them; smem: the kernel's LDS (C::Lds bytes).
-template <typename T, int RT, int CT, int ACT, bool FAST, bool SPLIT, bool Q4K>
+// FAST selects the register epilogue (activation ACT, a residual iff RES), otherwise the general one.
+template <typename T, int RT, int CT, int ACT, bool FAST, bool RES, bool SPLIT, bool Q4K>
 __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit& sp, char* smem) {
     typedef WideCfg<RT, CT, Q4K> C;
     typedef typename PipeMfma<T>::vec Vec;
@@ -388,16 +389,18 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
             const bool ok = col_ok & (row < p.m);  // no short-circuit: a select, not a branch
             return ok ? (uint32_t)(row * (uint32_t)ld + col) * 2u : kOff;
         };
-        // the residual loads of the first PD chunks go out first, those of chunk q + PD before chunk q's stores;
+        // RES: the residual loads of the first PD chunks go out first, those of chunk q + PD before chunk q's stores;
         // PD = every chunk where the registers allow
-        constexpr int PD = NQ * NR <= 32 ? NQ : 2;
+        constexpr int PD = !RES ? 1 : NQ * NR <= 32 ? NQ : 2;
         uint2 r2[PD][NR];
         auto load_res = [&](int q) __attribute__((always_inline)) {
+            if constexpr (RES) {
 #pragma unroll
-            for (int i = 0; i < NR; ++i) {
-                // (elements taken by index: a bit cast of an ext-vector element accessor (.y) read the wrong half)
-                const auto w = __builtin_amdgcn_raw_buffer_load_b64(rr, out_off(m0 + ER * q + RPI * i + rl, p.ldr), 0, 0);
-                r2[q % PD][i] = make_uint2(w[0], w[1]);
+                for (int i = 0; i < NR; ++i) {
+                    // (elements taken by index: a bit cast of an ext-vector element accessor (.y) read the wrong half)
+                    const auto w = __builtin_amdgcn_raw_buffer_load_b64(rr, out_off(m0 + ER * q + RPI * i + rl, p.ldr), 0, 0);
+                    r2[q % PD][i] = make_uint2(w[0], w[1]);
+                }
             }
         };
 #pragma unroll
@@ -416,9 +419,14 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
                     lo = __builtin_convertvector(__builtin_convertvector(lo, T2), f32x2);
                     hi = __builtin_convertvector(__builtin_convertvector(hi, T2), f32x2);
                 }
-                const uint2 rr2 = r2[q % PD][i];
-                lo = lo + f32x2{b[0], b[1]} + __builtin_convertvector(__builtin_bit_cast(T2, rr2.x), f32x2);
-                hi = hi + f32x2{b[2], b[3]} + __builtin_convertvector(__builtin_bit_cast(T2, rr2.y), f32x2);
+                if constexpr (RES) {
+                    const uint2 rr2 = r2[q % PD][i];
+                    lo = lo + f32x2{b[0], b[1]} + __builtin_convertvector(__builtin_bit_cast(T2, rr2.x), f32x2);
+                    hi = hi + f32x2{b[2], b[3]} + __builtin_convertvector(__builtin_bit_cast(T2, rr2.y), f32x2);
+                } else {
+                    lo = lo + f32x2{b[0], b[1]};
+                    hi = hi + f32x2{b[2], b[3]};
+                }
                 lo = f32x2{act_fast<ACT>(lo.x), act_fast<ACT>(lo.y)};
                 hi = f32x2{act_fast<ACT>(hi.x), act_fast<ACT>(hi.y)};
                 const i32x2 o = {__builtin_bit_cast(int, __builtin_convertvector(lo, T2)),
@@ -653,22 +661,47 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
     }
 }
 
-template <typename T, int RT, int CT, int ACT, bool FAST, bool SPLIT, bool Q4K = false>
+template <typename T, int RT, int CT, int ACT, bool FAST, bool RES, bool SPLIT, bool Q4K = false>
 __global__ __launch_bounds__(kWideThreads) void q8_wide_kernel(GemmParams p, WideSplit sp) {
     __shared__ __attribute__((aligned(1024))) char smem[WideCfg<RT, CT, Q4K>::Lds];
-    wide_tiles<T, RT, CT, ACT, FAST, SPLIT, Q4K>(p, sp, smem);
+    wide_tiles<T, RT, CT, ACT, FAST, RES, SPLIT, Q4K>(p, sp, smem);
 }
 
-// Two column ranges in one launch: 256 x 256 tiles on pa's columns, then 128 x 256 tiles on pb's (the column split
-// of the launch plans). A workgroup takes its share of the first and then of the second; the second range's first
-// loads follow the first range's epilogue without a kernel boundary between them.
-template <typename T, int ACT, bool FAST, bool Q4K>
-__global__ __launch_bounds__(kWideThreads) void q8_wide_pair_kernel(GemmParams pa, GemmParams pb) {
+// Two column ranges in one launch: 256 x 256 tiles on pa's columns, 128 x 256 tiles on pb's (the column split of
+// the launch plans). A workgroup takes its share of both ranges, the second range's first loads following the first
+// range's epilogue without a kernel boundary between them. The workgroups with (blockIdx.x & swap) != 0 take pb's
+// share first, so that their first epilogue (and its burst of output writes) falls in the others' main loop instead
+// of every workgroup writing its first tile at once.
+template <typename T, int ACT, bool FAST, bool RES, bool Q4K>
+__global__ __launch_bounds__(kWideThreads) void q8_wide_pair_kernel(GemmParams pa, GemmParams pb, unsigned swap) {
     constexpr int kLds = WideCfg<8, 2, Q4K>::Lds > WideCfg<4, 2, Q4K>::Lds ? WideCfg<8, 2, Q4K>::Lds : WideCfg<4, 2, Q4K>::Lds;
     __shared__ __attribute__((aligned(1024))) char smem[kLds];
     const WideSplit whole{0, 0, 0, 0, nullptr, nullptr};
-    wide_tiles<T, 8, 2, ACT, FAST, false, Q4K>(pa, whole, smem);
-    wide_tiles<T, 4, 2, ACT, FAST, false, Q4K>(pb, whole, smem);
+    const int first = (blockIdx.x & swap) != 0 ? 1 : 0;
+    for (int pass = 0; pass < 2; ++pass) {
+        if ((pass ^ first) == 0)
+            wide_tiles<T, 8, 2, ACT, FAST, RES, false, Q4K>(pa, whole, smem);
+        else
+            wide_tiles<T, 4, 2, ACT, FAST, RES, false, Q4K>(pb, whole, smem);
+    }
+}
+
+// f(activation, residual present) as compile-time constants, for the register epilogue's activations (the others
+// take the general epilogue)
+template <typename F>
+void with_fast_epilogue(const GemmParams& p, F&& f) {
+    auto with_act = [&](auto act) {
+        if (p.res)
+            f(act, std::true_type{});
+        else
+            f(act, std::false_type{});
+    };
+    if (p.act == IDOLQ_ACT_GELU_TANH)
+        with_act(std::integral_constant<int, IDOLQ_ACT_GELU_TANH>{});
+    else if (p.act == IDOLQ_ACT_RELU)
+        with_act(std::integral_constant<int, IDOLQ_ACT_RELU>{});
+    else
+        with_act(std::integral_constant<int, IDOLQ_ACT_NONE>{});
 }
 
 // The register epilogue addresses y and the residual with 31-bit byte offsets (buffer accesses).
@@ -686,20 +719,19 @@ int launch_wide_s(GemmParams p, const WideSplit& sp, hipStream_t stream) {
     const bool fast = p.y_vec4 && p.n % 4 == 0 && below_2gb(p) && p.y_dt == kYdt && (!p.res || p.res_dt == kYdt) &&
                       (!p.bias || p.bias_dt == IDOLQ_F32) &&
                       (p.act == IDOLQ_ACT_NONE || p.act == IDOLQ_ACT_GELU_TANH || p.act == IDOLQ_ACT_RELU);
-    // the register epilogue's activation is a template argument; other activations take the general path
     if (!fast)
-        hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, IDOLQ_ACT_NONE, false, SPLIT, Q4K>), grid, block, 0, stream, p, sp);
-    else if (p.act == IDOLQ_ACT_GELU_TANH)
-        hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, IDOLQ_ACT_GELU_TANH, true, SPLIT, Q4K>), grid, block, 0, stream, p, sp);
-    else if (p.act == IDOLQ_ACT_RELU)
-        hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, IDOLQ_ACT_RELU, true, SPLIT, Q4K>), grid, block, 0, stream, p, sp);
+        hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, IDOLQ_ACT_NONE, false, false, SPLIT, Q4K>), grid, block, 0, stream, p, sp);
     else
-        hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, IDOLQ_ACT_NONE, true, SPLIT, Q4K>), grid, block, 0, stream, p, sp);
+        with_fast_epilogue(p, [&](auto act, auto res) {
+            hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, decltype(act)::value, true, decltype(res)::value, SPLIT, Q4K>), grid,
+                               block, 0, stream, p, sp);
+        });
     return check_launch("q8_wide_kernel");
 }
 
+// swap: see q8_wide_pair_kernel (1: the workgroups on every other XCD start with the 128-row range)
 template <typename T, bool Q4K>
-int launch_wide_pair(GemmParams pa, GemmParams pb, int grid, hipStream_t stream) {
+int launch_wide_pair(GemmParams pa, GemmParams pb, int grid, hipStream_t stream, unsigned swap = 1) {
     pa.tiles_m = (pa.m + 255) / 256;
     pa.tiles_n = (pa.n + 255) / 256;
     pb.tiles_m = (pb.m + 127) / 128;
@@ -712,13 +744,12 @@ int launch_wide_pair(GemmParams pa, GemmParams pb, int grid, hipStream_t stream)
                       (p.act == IDOLQ_ACT_NONE || p.act == IDOLQ_ACT_GELU_TANH || p.act == IDOLQ_ACT_RELU);
     const dim3 g(grid), block(kWideThreads);
     if (!fast)
-        hipLaunchKernelGGL((q8_wide_pair_kernel<T, IDOLQ_ACT_NONE, false, Q4K>), g, block, 0, stream, pa, pb);
-    else if (p.act == IDOLQ_ACT_GELU_TANH)
-        hipLaunchKernelGGL((q8_wide_pair_kernel<T, IDOLQ_ACT_GELU_TANH, true, Q4K>), g, block, 0, stream, pa, pb);
-    else if (p.act == IDOLQ_ACT_RELU)
-        hipLaunchKernelGGL((q8_wide_pair_kernel<T, IDOLQ_ACT_RELU, true, Q4K>), g, block, 0, stream, pa, pb);
+        hipLaunchKernelGGL((q8_wide_pair_kernel<T, IDOLQ_ACT_NONE, false, false, Q4K>), g, block, 0, stream, pa, pb, swap);
     else
-        hipLaunchKernelGGL((q8_wide_pair_kernel<T, IDOLQ_ACT_NONE, true, Q4K>), g, block, 0, stream, pa, pb);
+        with_fast_epilogue(p, [&](auto act, auto res) {
+            hipLaunchKernelGGL((q8_wide_pair_kernel<T, decltype(act)::value, true, decltype(res)::value, Q4K>), g, block, 0,
+                               stream, pa, pb, swap);
+        });
     return check_launch("q8_wide_pair_kernel");
 }
 
