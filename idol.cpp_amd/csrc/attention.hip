@@ -103,11 +103,11 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_hd64(AttnParams p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[t][r] = 0.0f;
 
-    // The running maximum mc is kept in the scaled (base-2) domain and raised lazily: only when a tile's scores
-    // exceed it by more than 8, so probabilities stay below 2^8 (well inside fp16) and most tiles skip the
-    // rescaling of o and l. Scores are turned into u = s * c - mc first (the maximum is taken over u: products of
-    // an FMA need no NaN canonicalization, MFMA results would). l is summed per lane (half of each query's keys)
-    // and combined at the end.
+    // The running maximum mc is kept in the scaled (base-2) domain: the first tile's maximum, raised lazily
+    // afterwards, only for a tile whose fp16 probabilities sum to 2^15 or more (some score more than 10 above mc),
+    // so every probability stays inside fp16 and most tiles neither take a maximum nor rescale o and l. Scores are
+    // turned into u = s * c - mc first (a maximum is taken over u: products of an FMA need no NaN canonicalization,
+    // MFMA results would). l is summed per lane (half of each query's keys) and combined at the end.
     const float c = p.scale_log2;
     float mc = -INFINITY, l_part = 0.0f;
     const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
@@ -200,6 +200,22 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_hd64(AttnParams p) {
                 s[st] = AttnMfma<T>::run(a, qf[c4], c4 == 0 ? f32x16{} : s[st]);
             }
         }
+        // The V^T operands of the product (chunk (st, kc), d block t): those of the first 32 keys are read now, so
+        // that their LDS latency passes under the softmax's vector work, the others before the product (under the
+        // first half's MFMAs), instead of each P * V MFMA waiting for its own read.
+        f16x8 va[2][2][2];
+        auto read_v = [&](int st) __attribute__((always_inline)) {
+#pragma unroll
+            for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const int d = t * 32 + (lane & 31), key0 = st * 32 + 16 * kc + 4 * half;
+                    const uint2 lo = *reinterpret_cast<const uint2*>(&vt_lds[buf][d * kVPitch + key0]);
+                    const uint2 hi = *reinterpret_cast<const uint2*>(&vt_lds[buf][d * kVPitch + key0 + 8]);
+                    va[st][kc][t] = __builtin_bit_cast(f16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                }
+        };
+        read_v(0);
         if (MASK) {
             // keys past lk get no weight
             const int valid = (int)(p.lk - j0);
@@ -217,14 +233,40 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_hd64(AttnParams p) {
         }
 #pragma unroll
         for (int i = 0; i < 32; ++i) s[i >> 4][i & 15] = fmaf(s[i >> 4][i & 15], c, -mc);
-        if (!FIRST) {
-            // maximum over this lane's 32 values, then over the query's other 32 (lane ^ 32)
-            float mx = -INFINITY;
+        // The probabilities as fp16 MFMA operands, chunk (st, kc) holding keys st*32 + 16 kc + ..., and this lane's
+        // sum of them as rounded (fp32 dot products with ones).
+        f16x8 pf[2][2];
+        float lt;
+        auto probabilities = [&]() __attribute__((always_inline)) {
+            float ls[2] = {0.0f, 0.0f};  // two dependent chains of dot products instead of one
 #pragma unroll
-            for (int i = 0; i < 32; i += 2) mx = fmaxf(mx, fmaxf(s[i >> 4][i & 15], s[i >> 4][(i & 15) + 1]));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const bool raise = mx > 8.0f;
-            if (__builtin_amdgcn_ballot_w64(raise) != 0) {  // a wave-uniform branch: most tiles skip it
+            for (int st = 0; st < 2; ++st)
+#pragma unroll
+                for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+                    for (int e = 0; e < 8; e += 2) {
+                        const f32x2 pe = {__builtin_amdgcn_exp2f(s[st][8 * kc + e]),
+                                          __builtin_amdgcn_exp2f(s[st][8 * kc + e + 1])};
+                        const f16x2 hp = __builtin_convertvector(pe, f16x2);
+                        pf[st][kc][e] = hp.x;
+                        pf[st][kc][e + 1] = hp.y;
+                        ls[st] = __builtin_amdgcn_fdot2(hp, ones, ls[st], false);
+                    }
+            lt = ls[0] + ls[1];
+        };
+        probabilities();
+        if (!FIRST) {
+            // The maximum is not taken per tile: a score more than 16 above mc overflows its fp16 probability (inf)
+            // and so the sum. A sum that is not below 2^15 (inf or NaN included; every probability below 2^8 keeps
+            // it under 2^13) sends the wave through the rare path (a wave-uniform branch): the lanes whose query's
+            // maximum (over both lanes of the query, lane ^ 32) exceeds mc by more than 8 raise mc to it, scale o
+            // and l by 2^-delta, and the tile's probabilities are recomputed.
+            if (__builtin_amdgcn_ballot_w64(!(lt < 32768.0f)) != 0) {
+                float mx = -INFINITY;
+#pragma unroll
+                for (int i = 0; i < 32; i += 2) mx = fmaxf(mx, fmaxf(s[i >> 4][i & 15], s[i >> 4][(i & 15) + 1]));
+                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                const bool raise = mx > 8.0f;
                 const float delta = raise ? mx : 0.0f;
                 const float alpha = __builtin_amdgcn_exp2f(-delta);
                 l_part *= alpha;
@@ -235,8 +277,10 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_hd64(AttnParams p) {
 #pragma unroll
                 for (int i = 0; i < 32; ++i) s[i >> 4][i & 15] -= delta;
                 mc += delta;
+                probabilities();
             }
         }
+        l_part += lt;
 
         // O^T += V^T * P^T over 4 chunks of 16 keys. Chunk (st, kc) uses accumulator elements r = 8 kc + e of
         // sub-tile st; slot 8 * half + e of the MFMA's k holds key st*32 + 16 kc + 8 (e / 4) + 4 half + e % 4.
@@ -247,31 +291,13 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_hd64(AttnParams p) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) o[t][r] *= down;
         }
+        read_v(1);
 #pragma unroll
         for (int st = 0; st < 2; ++st)
 #pragma unroll
-            for (int kc = 0; kc < 2; ++kc) {
-                f16x8 pf;
+            for (int kc = 0; kc < 2; ++kc)
 #pragma unroll
-                for (int e = 0; e < 8; e += 2) {
-                    const f32x2 pe = {__builtin_amdgcn_exp2f(s[st][8 * kc + e]),
-                                      __builtin_amdgcn_exp2f(s[st][8 * kc + e + 1])};
-                    const f16x2 hp = __builtin_convertvector(pe, f16x2);
-                    pf[e] = hp.x;
-                    pf[e + 1] = hp.y;
-                    // the normalizer sums the probabilities as rounded for the product
-                    l_part = __builtin_amdgcn_fdot2(hp, ones, l_part, false);
-                }
-                const int key0 = st * 32 + 16 * kc + 4 * half;
-#pragma unroll
-                for (int t = 0; t < 2; ++t) {
-                    const int d = t * 32 + (lane & 31);
-                    const uint2 lo = *reinterpret_cast<const uint2*>(&vt_lds[buf][d * kVPitch + key0]);
-                    const uint2 hi = *reinterpret_cast<const uint2*>(&vt_lds[buf][d * kVPitch + key0 + 8]);
-                    const f16x8 va = __builtin_bit_cast(f16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
-                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pf, o[t], 0, 0, 0);
-                }
-            }
+                for (int t = 0; t < 2; ++t) o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[st][kc][t], pf[st][kc], o[t], 0, 0, 0);
         if (kWideV && vexp != 0) {
             const float up = __builtin_bit_cast(float, (uint32_t)(127 + vexp) << 23);
 #pragma unroll

@@ -205,6 +205,30 @@ def test_self_attention_seq4096_sample():
     assert np.isfinite(got).all()
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_attention_raises_the_running_maximum(dtype):
+    # scores that grow along the keys (key rows scaled from 0.5 to 4, positive means) and, in head 0, one key whose
+    # scores exceed every earlier one by far: the first tile's maximum must be raised again and again (without that,
+    # later probabilities would leave fp16), against the oracle on the upcast inputs at 1e-3
+    rng = np.random.default_rng(27)
+    lq, lk, heads, hd = 160, 700, 2, 64
+    dim = heads * hd
+    q = rng.normal(0.5, 1, (lq, dim)).astype(np.float32)
+    k = (rng.normal(0.5, 1, (lk, dim)) * np.linspace(0.5, 4, lk)[:, None]).astype(np.float32)
+    k[450, :hd] = 6.0
+    v = rng.normal(0, 1, (lk, dim)).astype(np.float32)
+    qd, kd, vd = (to_dev(a).to(dtype) for a in (q, k, v))
+    out = torch.empty((lq, dim), device=DEV, dtype=dtype)
+    L.attention(qd, kd, vd, 1, lq, lk, heads, hd, dim, dim, 0, 0, out, dim, 0)
+    ref = O.attention(qd.float().cpu().numpy(), kd.float().cpu().numpy(), vd.float().cpu().numpy(), lq, lk, dim, dim,
+                      heads, hd)
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    for h in range(heads):
+        cols = slice(h * hd, (h + 1) * hd)
+        assert norm_rel(got[:, cols], torch.from_numpy(ref[:, cols]).to(dtype).float().numpy()) < 1e-3, h
+
+
 def test_attention_bf16_values_beyond_fp16_range():
     # bf16 V holds values far beyond fp16's 65504 (the reference's fp32 attention takes them): the tiles that hold
     # them are staged with an exact power-of-two scale, so the output stays finite and within the 16-bit bar, with
