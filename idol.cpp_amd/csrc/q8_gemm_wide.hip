@@ -38,6 +38,7 @@
 #include "q8_dma.h"
 
 #include <algorithm>
+#include <numeric>
 #include <cstdlib>
 #include <string>
 #include <type_traits>
@@ -63,6 +64,12 @@ struct WideSplit {
     int L, R;     // stream-K ranges over the remaining tiles' stages; null part: whole tiles only
     float* part;  // 2 G partial tiles: slot 2 r + f holds range r's first (f = 0) or last (f = 1) part
     int* count;   // G counters, zero between launches (the workspace's first bytes)
+    // Order of the split tiles. Ranges whose starts differ by a multiple of the tile depth run at the same k offset
+    // (with all ranges of L stages, ranges r and r + S / gcd(L, S) are ph = L / gcd(L, S) tiles apart): split tile
+    // tl is walked as tile (tl % ph) * (nsplit / ph) + tl / ph, so that the in-phase ranges of one XCD take
+    // neighbouring tiles, in groups of gh row tiles walked column by column (gh = 4: blocks of 4 x 2 tiles), and read
+    // the same activation and weight rows at the same time (0 / 1: tiles in range order, groups of 8).
+    int ph, gh;
 };
 
 // Q4K: the weights are GGUF Q4_K super-blocks, row-major (one row: k / 256 blocks of 144 bytes: fp16 d, fp16 dmin,
@@ -525,11 +532,10 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
         run_step(1, [](int) {});
         __builtin_amdgcn_sched_barrier(0);
     };
-    // tile t: groups of 8 row tiles walked column by column
-    auto tile_at = [&](int t, int& m0, int& n0) __attribute__((always_inline)) {
-        constexpr int G8 = 8;
-        const int per_group = G8 * p.tiles_n, group = t / per_group, first = group * G8;
-        const int gm = min(p.tiles_m - first, G8), in_group = t - group * per_group;
+    // tile t: groups of gh row tiles walked column by column
+    auto tile_at = [&](int t, int& m0, int& n0, int gh = 8) __attribute__((always_inline)) {
+        const int per_group = gh * p.tiles_n, group = t / per_group, first = group * gh;
+        const int gm = min(p.tiles_m - first, gh), in_group = t - group * per_group;
         m0 = __builtin_amdgcn_readfirstlane((first + in_group % gm) * C::BM);
         n0 = __builtin_amdgcn_readfirstlane((in_group / gm) * C::BN);
     };
@@ -571,7 +577,9 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
             const int tl = (int)(i / S), k0 = (int)(i - (int64_t)tl * S);
             const int n = (int)min((int64_t)(S - k0), end - i);
             int m0, n0;
-            tile_at(sp.dp + tl, m0, n0);
+            const int nsplit = ntiles - sp.dp;
+            const int v = sp.ph > 1 ? (tl % sp.ph) * (nsplit / sp.ph) + tl / sp.ph : tl;
+            tile_at(sp.dp + v, m0, n0, sp.gh > 0 ? sp.gh : 8);
             run_segment(m0, n0, k0, n);
             if (n < S) {
                 const int64_t t0 = (int64_t)tl * S;
@@ -843,7 +851,12 @@ int launch_wide_dtype(GemmParams p, void* workspace, size_t workspace_bytes, hip
     if (best_split) {
         const long dp = tiles / cus * cus, units = (tiles - dp) * S;
         sp = WideSplit{(int)cus, (int)dp, (int)(units / cus), (int)(units % cus),
-                       reinterpret_cast<float*>(static_cast<char*>(workspace) + kCountBytes), static_cast<int*>(workspace)};
+                       reinterpret_cast<float*>(static_cast<char*>(workspace) + kCountBytes), static_cast<int*>(workspace), 1, 8};
+        // in-phase ranges (all of L stages) on neighbouring tiles; groups of 4 row tiles when every tile is split
+        // (the walk of the whole tiles is then not involved)
+        const long g = std::gcd((long)sp.L, S), nsplit = tiles - dp;
+        if (sp.R == 0 && sp.L > 0 && sp.L / g > 1 && nsplit % (sp.L / g) == 0) sp.ph = (int)(sp.L / g);
+        if (dp == 0) sp.gh = 4;
     }
     if (best_shape == 0) return launch_wide_s<T, 8, 2, false, Q4K>(p, sp, stream);
     return launch_shape<T, Q4K, 4, 2>(p, sp, best_split, stream);
