@@ -292,12 +292,16 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_hd64(AttnParams p) {
                 for (int r = 0; r < 16; ++r) o[t][r] *= down;
         }
         read_v(1);
+        // raised wave priority while the product issues, so that the SIMD's other waves (in their softmax) do not
+        // delay its MFMAs (1-2% on the self-attention shape)
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int st = 0; st < 2; ++st)
 #pragma unroll
             for (int kc = 0; kc < 2; ++kc)
 #pragma unroll
                 for (int t = 0; t < 2; ++t) o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[st][kc][t], pf[st][kc], o[t], 0, 0, 0);
+        __builtin_amdgcn_s_setprio(0);
         if (kWideV && vexp != 0) {
             const float up = __builtin_bit_cast(float, (uint32_t)(127 + vexp) << 23);
 #pragma unroll

@@ -3,6 +3,7 @@
 #include "common.h"
 
 #include <cstdio>
+#include <type_traits>
 
 namespace idolq {
 
@@ -119,6 +120,43 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const void* __restric
     if (qsum) qsum[id] = sum;
 }
 
+// The same rule for 16-bit activations with 16-byte aligned rows, four threads per (row, 32-block): each loads 8 values
+// with one 16-byte load (consecutive lanes read consecutive bytes), the block's maximum comes from two exchanges
+// inside the group of four, and each thread writes its 8 codes (the first one the scale). No code sums.
+template <typename T>
+__global__ __launch_bounds__(256) void quantize_act16_kernel(const T* __restrict__ x, int64_t m, int64_t nb,
+                                                             int64_t ldx, int8_t* __restrict__ qa,
+                                                             float* __restrict__ scale) {
+    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t blocks = m * nb;
+    const bool ok = (id >> 2) < blocks;
+    const int64_t b = ok ? id >> 2 : blocks - 1;  // every lane takes part in the exchanges
+    const int qt = (int)(id & 3);
+    const int64_t r = b / nb, g = b - r * nb;
+    const uint4 raw = *reinterpret_cast<const uint4*>(x + r * ldx + g * kQ8Block + 8 * qt);
+    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint16_t h = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+        v[e] = std::is_same<T, __bf16>::value ? bf16_bits_to_float(h) : half_bits_to_float(h);
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    const float s = amax / 127.0f;
+    const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+    uint32_t word[2] = {0, 0};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) word[e >> 2] |= (uint32_t)(uint8_t)(int8_t)(int32_t)rintf(v[e] * inv) << (8 * (e & 3));
+    if (ok) {
+        *reinterpret_cast<uint2*>(qa + r * (nb * kQ8Block) + g * kQ8Block + 8 * qt) = make_uint2(word[0], word[1]);
+        if (qt == 0) scale[b] = s;
+    }
+}
+
 // ------------------------------------------------------------------------------------------------ elementwise
 __global__ __launch_bounds__(256) void activation_kernel(void* x, int dt, int64_t count, int act) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -200,6 +238,19 @@ int quantize_act_launch(const void* x, int x_dtype, int64_t m, int64_t k, int64_
                         int32_t* qsum, hipStream_t stream) {
     const int64_t nb = k / kQ8Block;
     if (m * nb == 0) return IDOLQ_OK;
+    const bool vec16 = !qsum && (x_dtype == IDOLQ_BF16 || x_dtype == IDOLQ_F16) &&
+                       reinterpret_cast<uintptr_t>(x) % 16 == 0 && (ldx * 2) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(qa) % 8 == 0;
+    if (vec16) {
+        const dim3 grid((unsigned)((4 * m * nb + 255) / 256));
+        if (x_dtype == IDOLQ_BF16)
+            hipLaunchKernelGGL(quantize_act16_kernel<__bf16>, grid, dim3(256), 0, stream, static_cast<const __bf16*>(x),
+                               m, nb, ldx, qa, scale);
+        else
+            hipLaunchKernelGGL(quantize_act16_kernel<_Float16>, grid, dim3(256), 0, stream,
+                               static_cast<const _Float16*>(x), m, nb, ldx, qa, scale);
+        return check_launch("quantize_act16_kernel");
+    }
     hipLaunchKernelGGL(quantize_act_kernel, dim3((unsigned)((m * nb + 255) / 256)), dim3(256), 0, stream, x, x_dtype, m,
                        nb, ldx, qa, scale, qsum);
     return check_launch("quantize_act_kernel");

@@ -65,6 +65,23 @@ def test_activation_quantization_is_bit_exact(golden, dtype):
     assert np.array_equal(qs.cpu().numpy(), rqs)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_activation_quantization_without_sums_is_bit_exact(dtype):
+    # without code sums, 16-bit rows take the four-threads-per-block quantizer (the INT8 GEMM's): the same codes and
+    # scales as the oracle, with an odd row count (a partial last workgroup), an all-zero block and ties to even
+    rng = np.random.default_rng(13)
+    a = rng.normal(0, 3, (301, 1536)).astype(np.float32)
+    a[7, 64:96] = 0.0
+    a[8, :32] = np.concatenate([[127.0], np.arange(31) * 0.5 - 7.5]).astype(np.float32)  # amax 127: x.5 ties
+    x = to_dev(a).to(dtype)
+    qa, sa, qs = L.quantize_act(x, with_qsum=False)
+    rqa, rsa, _ = O.quantize_act(x.float().cpu().numpy())
+    assert qs is None
+    assert np.array_equal(qa.cpu().numpy(), rqa)
+    assert np.array_equal(sa.cpu().numpy().view(np.uint32), rsa.view(np.uint32))
+    assert not qa[7, 64:96].any() and float(sa[7, 2]) == 0.0
+
+
 @pytest.mark.parametrize("m,n,k,off,cnt", [(70, 100, 352, 0, 100), (130, 200, 256, 16, 150), (5, 21, 32, 0, 21),
                                            (256, 384, 1536, 128, 256), (1, 7, 64, 0, 7)])
 def test_int8_mfma_block_dots_are_bit_exact(m, n, k, off, cnt):
