@@ -93,13 +93,13 @@ def mlp_inputs(torch, L, seed=0):
 
 
 class MlpBlock:
-    """The MLP block on preallocated buffers. DEQUANT reads the weights in the tiled Q8_0 layout (the same blocks,
-    reordered once at load time); INT8 and EXACT read the GGUF row-major blocks (INT8 with its workspace)."""
+    """The MLP block on preallocated buffers. DEQUANT and INT8 read the weights in the tiled Q8_0 layout (the same
+    blocks, reordered once at load time; INT8 with its workspace); EXACT reads the GGUF row-major blocks."""
 
     def __init__(self, torch, L, mode, inputs):
         self.L, self.mode = L, mode
         self.x, w_up, w_down, self.b_up, self.b_down = inputs
-        self.tiled = mode == L.MODE_DEQUANT
+        self.tiled = mode in (L.MODE_DEQUANT, L.MODE_INT8)
         self.w_up = L.tile_q8_0(w_up, H, D) if self.tiled else w_up
         self.w_down = L.tile_q8_0(w_down, D, H) if self.tiled else w_down
         self.h = torch.empty((M, H), device="cuda", dtype=torch.bfloat16)
@@ -230,8 +230,7 @@ def run_gpu(args):
                      "frac": achieved / PEAK_TFLOPS[arith], "traffic": traffic["mean"] if traffic else None,
                      "traffic_per_launch": traffic,
                      "algorithmic_bytes": {"up": ALG_BYTES_UP, "down": ALG_BYTES_DOWN},
-                     "kernel": "q8_wide_kernel" if args.mode == "dequant" else
-                               "q8_gemm_kernel" if args.mode == "exact" else "q8_gemm_int8_kernel",
+                     "kernel": "q8_gemm_kernel" if args.mode == "exact" else "q8_wide_kernel",
                      "launch_ms": {"up": up_ms, "down": down_ms},
                      "flop_per_launch": flop_gemm},
         "pct_int8_peak": value / PEAK_TFLOPS["int8"],
@@ -242,7 +241,8 @@ def run_gpu(args):
 
 def run_int8_block(args, inputs):
     """The MLP block in INT8 mode (the reference's integer kernel semantics: activations quantized per row and
-    32-block, int8 MFMA block dots, per-block fp32 scale fold) on the same inputs: per-GEMM launch time from HIP
+    32-block, int8 MFMA block dots, per-block fp32 scale fold; tiled weights, stream-K allowed) on the same inputs:
+    per-GEMM launch time from HIP
     events on the launch stream (activation quantization included, it is part of the mode), as TFLOP/s-equivalent
     and as a fraction of the int8 MFMA peak."""
     import torch

@@ -120,26 +120,39 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const void* __restric
     if (qsum) qsum[id] = sum;
 }
 
-// The same rule for 16-bit activations with 16-byte aligned rows, four threads per (row, 32-block): each loads 8 values
-// with one 16-byte load (consecutive lanes read consecutive bytes), the block's maximum comes from two exchanges
-// inside the group of four, and each thread writes its 8 codes (the first one the scale). No code sums.
-template <typename T>
+// The same rule for activations with 16-byte aligned rows, four threads per (row, 32-block): each loads its 8 values
+// with 16-byte loads (consecutive lanes read consecutive bytes), the block's maximum comes from two exchanges inside
+// the group of four, and each thread writes its 8 codes (the first one the scale). No code sums.
+// TILED (the layout of the GEMM on tiled weights): each block's codes in the order 0..7, 16..23, 8..15, 24..31 (the
+// k order of the tiled weights' MFMA fragments), and the scales stage-major: block g of row r at
+// (g / 2) * 2 m + 2 r + g % 2 (the two blocks of a 64-deep stage of consecutive rows are contiguous).
+// zero (TILED): nzero ints cleared on the side (the GEMM's tile counters).
+template <typename T, bool TILED>
 __global__ __launch_bounds__(256) void quantize_act16_kernel(const T* __restrict__ x, int64_t m, int64_t nb,
                                                              int64_t ldx, int8_t* __restrict__ qa,
-                                                             float* __restrict__ scale) {
+                                                             float* __restrict__ scale, int* __restrict__ zero,
+                                                             int nzero) {
     const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (TILED && zero)
+        for (int64_t i = id; i < nzero; i += (int64_t)gridDim.x * blockDim.x) zero[i] = 0;
     const int64_t blocks = m * nb;
     const bool ok = (id >> 2) < blocks;
     const int64_t b = ok ? id >> 2 : blocks - 1;  // every lane takes part in the exchanges
     const int qt = (int)(id & 3);
     const int64_t r = b / nb, g = b - r * nb;
-    const uint4 raw = *reinterpret_cast<const uint4*>(x + r * ldx + g * kQ8Block + 8 * qt);
-    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
     float v[8];
+    if constexpr (std::is_same<T, float>::value) {
+        const float4 lo = *reinterpret_cast<const float4*>(x + r * ldx + g * kQ8Block + 8 * qt);
+        const float4 hi = *reinterpret_cast<const float4*>(x + r * ldx + g * kQ8Block + 8 * qt + 4);
+        v[0] = lo.x, v[1] = lo.y, v[2] = lo.z, v[3] = lo.w, v[4] = hi.x, v[5] = hi.y, v[6] = hi.z, v[7] = hi.w;
+    } else {
+        const uint4 raw = *reinterpret_cast<const uint4*>(x + r * ldx + g * kQ8Block + 8 * qt);
+        const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const uint16_t h = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
-        v[e] = std::is_same<T, __bf16>::value ? bf16_bits_to_float(h) : half_bits_to_float(h);
+        for (int e = 0; e < 8; ++e) {
+            const uint16_t h = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+            v[e] = std::is_same<T, __bf16>::value ? bf16_bits_to_float(h) : half_bits_to_float(h);
+        }
     }
     float amax = 0.0f;
 #pragma unroll
@@ -152,8 +165,9 @@ __global__ __launch_bounds__(256) void quantize_act16_kernel(const T* __restrict
 #pragma unroll
     for (int e = 0; e < 8; ++e) word[e >> 2] |= (uint32_t)(uint8_t)(int8_t)(int32_t)rintf(v[e] * inv) << (8 * (e & 3));
     if (ok) {
-        *reinterpret_cast<uint2*>(qa + r * (nb * kQ8Block) + g * kQ8Block + 8 * qt) = make_uint2(word[0], word[1]);
-        if (qt == 0) scale[b] = s;
+        const int pos = TILED ? 8 * (2 * (qt & 1) + (qt >> 1)) : 8 * qt;
+        *reinterpret_cast<uint2*>(qa + r * (nb * kQ8Block) + g * kQ8Block + pos) = make_uint2(word[0], word[1]);
+        if (qt == 0) scale[TILED ? (g >> 1) * 2 * m + 2 * r + (g & 1) : b] = s;
     }
 }
 
@@ -234,6 +248,25 @@ unsigned grid_for(int64_t items, int threads = 256) {
 
 }  // namespace
 
+// The tiled-GEMM layout of the INT8 mode (quantize_act16_kernel<T, true>): x rows 16-byte aligned, k a multiple of 64.
+int quantize_act_tiled_launch(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, int8_t* qa, float* scale,
+                              int* zero, int nzero, hipStream_t stream) {
+    const int64_t nb = k / kQ8Block;
+    if (m * nb == 0) return IDOLQ_OK;
+    const dim3 grid((unsigned)((4 * m * nb + 255) / 256));
+    if (x_dtype == IDOLQ_BF16)
+        hipLaunchKernelGGL((quantize_act16_kernel<__bf16, true>), grid, dim3(256), 0, stream,
+                           static_cast<const __bf16*>(x), m, nb, ldx, qa, scale, zero, nzero);
+    else if (x_dtype == IDOLQ_F16)
+        hipLaunchKernelGGL((quantize_act16_kernel<_Float16, true>), grid, dim3(256), 0, stream,
+                           static_cast<const _Float16*>(x), m, nb, ldx, qa, scale, zero, nzero);
+    else
+        hipLaunchKernelGGL((quantize_act16_kernel<float, true>), grid, dim3(256), 0, stream, static_cast<const float*>(x),
+                           m, nb, ldx, qa, scale, zero, nzero);
+    return check_launch("quantize_act16_kernel");
+}
+
+
 int quantize_act_launch(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, int8_t* qa, float* scale,
                         int32_t* qsum, hipStream_t stream) {
     const int64_t nb = k / kQ8Block;
@@ -244,11 +277,11 @@ int quantize_act_launch(const void* x, int x_dtype, int64_t m, int64_t k, int64_
     if (vec16) {
         const dim3 grid((unsigned)((4 * m * nb + 255) / 256));
         if (x_dtype == IDOLQ_BF16)
-            hipLaunchKernelGGL(quantize_act16_kernel<__bf16>, grid, dim3(256), 0, stream, static_cast<const __bf16*>(x),
-                               m, nb, ldx, qa, scale);
+            hipLaunchKernelGGL((quantize_act16_kernel<__bf16, false>), grid, dim3(256), 0, stream,
+                               static_cast<const __bf16*>(x), m, nb, ldx, qa, scale, nullptr, 0);
         else
-            hipLaunchKernelGGL(quantize_act16_kernel<_Float16>, grid, dim3(256), 0, stream,
-                               static_cast<const _Float16*>(x), m, nb, ldx, qa, scale);
+            hipLaunchKernelGGL((quantize_act16_kernel<_Float16, false>), grid, dim3(256), 0, stream,
+                               static_cast<const _Float16*>(x), m, nb, ldx, qa, scale, nullptr, 0);
         return check_launch("quantize_act16_kernel");
     }
     hipLaunchKernelGGL(quantize_act_kernel, dim3((unsigned)((m * nb + 255) / 256)), dim3(256), 0, stream, x, x_dtype, m,

@@ -62,7 +62,10 @@ int launch_pipe(GemmParams p, int xt, hipStream_t stream);
 // wide_workspace_bytes() (zero-filled before first use) the leftover tiles' k stages may be split over the CUs.
 bool wide_eligible(const GemmParams& p, int xt, int mode);
 size_t wide_workspace_bytes();
+constexpr size_t kWideCountBytes = 4096;  // the tile counters at the start of that workspace (zero between launches)
 int launch_wide(GemmParams p, int xt, void* workspace, size_t workspace_bytes, hipStream_t stream);
+// The INT8 mode on tiled weights (p.qa, p.sa from the tiled quantizer); workspace as launch_wide's (may be null).
+int launch_wide_i8(GemmParams p, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 // The small-m form (q8_gemv.hip): m <= kGemvMaxRows activation rows on GGUF row-major weights (k % 256 == 0, 16-byte
 // aligned), DEQUANT on 16-bit activations or EXACT; 16 weight rows per workgroup, the depth split over 8 waves.

@@ -775,9 +775,19 @@ int launch_int8(GemmParams p, bool w4, hipStream_t stream) {
 
 }  // namespace
 
-// Quantizes activations for the int8 path (q8_aux.hip).
+// Quantizes activations for the int8 path (q8_aux.hip); the tiled variant writes the layout of the tiled INT8 GEMM.
 int quantize_act_launch(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, int8_t* qa, float* scale,
                         int32_t* qsum, hipStream_t stream);
+int quantize_act_tiled_launch(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, int8_t* qa, float* scale,
+                              int* zero, int nzero, hipStream_t stream);
+
+// INT8 scratch: the activation codes (m x k bytes), then the scales (m x k / 32 fp32, 16 bytes of padding), each
+// rounded up to 256 bytes; the tiled path may use the rest as the stream-K workspace.
+size_t int8_prefix_bytes(int64_t m, int64_t k) {
+    const size_t qa = ((size_t)m * (size_t)k + 255) / 256 * 256;
+    const size_t sa = ((size_t)m * (size_t)(k / kQ8Block) * sizeof(float) + 16 + 255) / 256 * 256;
+    return qa + sa;
+}
 
 }  // namespace idolq
 
@@ -786,8 +796,8 @@ using namespace idolq;
 extern "C" size_t idolq_q8_0_gemm_workspace(int64_t m, int64_t k, int mode) {
     if (mode == IDOLQ_MODE_DEQUANT) return wide_workspace_bytes();
     if (mode != IDOLQ_MODE_INT8 || m <= 0 || k <= 0 || k % kQ8Block) return 0;
-    const size_t qa = ((size_t)m * (size_t)k + 255) / 256 * 256;
-    return qa + (size_t)m * (size_t)(k / kQ8Block) * sizeof(float);
+    // the scratch of either INT8 path, plus the stream-K workspace the tiled path can use after it
+    return int8_prefix_bytes(m, k) + wide_workspace_bytes();
 }
 
 extern "C" int idolq_q8_0_gemm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* w,
@@ -814,8 +824,8 @@ extern "C" int idolq_q8_0_gemm(const void* x, int x_dtype, int64_t m, int64_t k,
     if (mode == IDOLQ_MODE_DEQUANT && x_dtype == IDOLQ_F32)
         return fail(IDOLQ_EINVAL, "DEQUANT mode takes bf16 or fp16 activations");
     const bool tiled = (flags & IDOLQ_FLAG_TILED_WEIGHTS) != 0;
-    if (tiled && (mode != IDOLQ_MODE_DEQUANT || k % 64 || n_offset % 32))
-        return fail(IDOLQ_EINVAL, "tiled weights need DEQUANT mode, k a multiple of 64 and n_offset a multiple of 32");
+    if (tiled && (mode == IDOLQ_MODE_EXACT || k % 64 || n_offset % 32))
+        return fail(IDOLQ_EINVAL, "tiled weights need DEQUANT or INT8 mode, k a multiple of 64 and n_offset a multiple of 32");
     if (m == 0 || n == 0) return IDOLQ_OK;  // empty input: nothing to read or write (pointers may be null)
     if (!x || !w || !y) return fail(IDOLQ_EINVAL, "x, w and y must be non-null");
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -848,12 +858,30 @@ extern "C" int idolq_q8_0_gemm(const void* x, int x_dtype, int64_t m, int64_t k,
               (!residual || (reinterpret_cast<uintptr_t>(residual) % 16 == 0 && ((size_t)ldr * rsz) % 16 == 0));
 
     if (mode == IDOLQ_MODE_INT8) {
-        const size_t need = idolq_q8_0_gemm_workspace(m, k, mode);
+        // at least the codes and scales; beyond them the tiled path may split tiles over the CUs
+        const size_t need = int8_prefix_bytes(m, k);
         if (!workspace || workspace_bytes < need)
             return fail(IDOLQ_EINVAL, "INT8 mode needs a workspace of idolq_q8_0_gemm_workspace() bytes");
         if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return fail(IDOLQ_EINVAL, "workspace must be 16-byte aligned");
         int8_t* qa = static_cast<int8_t*>(workspace);
         float* sa = reinterpret_cast<float*>(static_cast<char*>(workspace) + ((size_t)m * (size_t)k + 255) / 256 * 256);
+        if (tiled) {
+            const size_t xsz = dtype_size(x_dtype);
+            if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || ((size_t)ldx * xsz) % 16 != 0 ||
+                (reinterpret_cast<uintptr_t>(w) & 15) != 0)
+                return fail(IDOLQ_EINVAL, "the tiled INT8 GEMM needs 16-byte aligned activation rows and weights");
+            if (p.groups <= 0) return fail(IDOLQ_EINVAL, "tiled weights: n_total exceeds the layout");
+            // the stream-K workspace after the scratch: its tile counters are cleared by the quantizer (the caller's
+            // workspace need not be zero)
+            char* rest = static_cast<char*>(workspace) + need;
+            const bool has_rest = workspace_bytes >= need + wide_workspace_bytes();
+            int rc = quantize_act_tiled_launch(x, x_dtype, m, k, ldx, qa, sa, has_rest ? reinterpret_cast<int*>(rest) : nullptr,
+                                               has_rest ? (int)(kWideCountBytes / sizeof(int)) : 0, s);
+            if (rc) return rc;
+            p.qa = qa;
+            p.sa = sa;
+            return launch_wide_i8(p, has_rest ? rest : nullptr, has_rest ? workspace_bytes - need : 0, s);
+        }
         int rc = quantize_act_launch(x, x_dtype, m, k, ldx, qa, sa, nullptr, s);
         if (rc) return rc;
         p.qa = qa;

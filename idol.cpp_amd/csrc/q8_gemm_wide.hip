@@ -77,17 +77,19 @@ struct WideSplit {
 // super-block (j = stage % 4), whose codes are the low and the high nibbles of the same 32 bytes 16 + 32 j .. of the
 // block. Per 32-row group and stage a wave loads those 32 bytes of each row (1 KB, lane l: row l % 32, bytes
 // 16 (l / 32) .. + 15) and the rows' 16-byte headers (512 bytes), straight from the row-major bytes.
-template <int RT, int CT, bool Q4K = false>
+// I8 (the INT8 mode): a stage of activations is BM rows x 64 int8 codes, then the rows' two fp32 block scales.
+template <int RT, int CT, bool Q4K = false, bool I8 = false>
 struct WideCfg {
     static constexpr int BM = 32 * RT, BN = 128 * CT;
-    static constexpr int ABuf = BM * 128;            // one stage of activations: BM rows x 64 16-bit values
+    static constexpr int ABuf = I8 ? BM * 72 : BM * 128;  // one stage of activations: BM rows x 64 16-bit values
     static constexpr int WCode = Q4K ? 1024 : 2048;  // one 32-row group's codes per stage
     static constexpr int WScale = Q4K ? 512 : 128;   // and its scales (Q4_K: the super-block headers)
     static constexpr int WWave = CT * (WCode + WScale);  // one stage of one wave's weight groups: codes, then scales
     static constexpr int WBuf = 4 * WWave;
     static constexpr int WBase = 3 * ABuf;
     static constexpr int Lds = WBase + 3 * WBuf;
-    static constexpr int DA = BM / 32;               // activation loads (1 KB each) per wave per stage
+    // activation loads per wave per stage: 1 KB each; I8: BM / 64 of 1 KB and one of the rows' scales (256 bytes)
+    static constexpr int DA = I8 ? BM / 64 + 1 : BM / 32;
     static constexpr int DW = Q4K ? 2 * CT : 2 * CT + 1;  // weight loads per wave per stage
     static_assert(Lds <= 163840, "LDS budget");
 };
@@ -128,9 +130,10 @@ __device__ __forceinline__ void q4k_header(uint4 hd, int pair, float (&ab)[4]) {
 
 // The tiles of one launch shape (RT, CT), with this workgroup's share of them; smem: the kernel's LDS (C::Lds bytes).
 // FAST selects the register epilogue (activation ACT, a residual iff RES), otherwise the general one.
-template <typename T, int RT, int CT, int ACT, bool FAST, bool RES, bool SPLIT, bool Q4K>
+// I8: the INT8 mode (see run_segment_i8); T then only names the output type of the register epilogue.
+template <typename T, int RT, int CT, int ACT, bool FAST, bool RES, bool SPLIT, bool Q4K, bool I8 = false>
 __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit& sp, char* smem) {
-    typedef WideCfg<RT, CT, Q4K> C;
+    typedef WideCfg<RT, CT, Q4K, I8> C;
     typedef typename PipeMfma<T>::vec Vec;
     typedef typename PipeMfma<T>::pair T2;
     constexpr int DA = C::DA, DW = C::DW;
@@ -142,6 +145,7 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
     const uint32_t lds0 = (uint32_t)(size_t)(lds_char*)smem;
     const char* xg;  // activations and weights of the segment's first stage
     const char* wg;
+    const char* sag = nullptr;  // I8: the activation scales of the segment's first stage
 
     // ---- per-tile load offsets (bytes, 32-bit)
     // activations: load j of this wave fills LDS 16-byte chunks u = 64 (DA wave + j) + lane of the stage buffer:
@@ -149,13 +153,29 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
     uint32_t a_off[DA], w_off[CT], ws_off, wh_off[CT];
     int seg_k0 = 0;  // Q4K: the segment's first stage (the stage's super-block and 32-group pair follow from it)
     auto start_tile = [&](int m0, int n0, int k0) __attribute__((always_inline)) {
-        xg = uniform_ptr(static_cast<const char*>(p.x) + (size_t)k0 * 128);
         wg = uniform_ptr(reinterpret_cast<const char*>(p.w) + (Q4K ? 0 : (size_t)k0 * kGroupBytes));
         seg_k0 = k0;
+        if constexpr (I8) {
+            // codes: row stride k bytes, stage s at byte 64 s; LDS chunk u = 64 (DA' wave + j) + lane (DA' = DA - 1)
+            // is row u / 4, position u % 4, holding chunk (u % 4) ^ ((row >> 2) & 3) of the row's 64 bytes
+            xg = uniform_ptr(reinterpret_cast<const char*>(p.qa) + (size_t)k0 * 64);
+            sag = uniform_ptr(reinterpret_cast<const char*>(p.sa) + (size_t)k0 * p.m * 8);
 #pragma unroll
-        for (int j = 0; j < DA; ++j) {
-            const int u = (wave * DA + j) * 64 + lane, row = u >> 3, c = (u & 7) ^ ((row >> 1) & 7);
-            a_off[j] = (uint32_t)((int64_t)min(m0 + row, p.m - 1) * p.ldx * 2 + c * 16);
+            for (int j = 0; j < DA - 1; ++j) {
+                const int u = (wave * (DA - 1) + j) * 64 + lane, row = u >> 2, c = (u & 3) ^ ((row >> 2) & 3);
+                a_off[j] = (uint32_t)((int64_t)min(m0 + row, p.m - 1) * p.k + c * 16);
+            }
+            // scales (stage-major: the stage's (block 2 s, 2 s + 1) pair of row r at 8 r): lane l < 16 of wave w takes
+            // rows 32 w + 2 l and + 1 with one 16-byte load from the first; rows from m on read row m - 1's bytes
+            // onward (the scale buffer is padded by 16 bytes), feeding only outputs that are never stored
+            a_off[DA - 1] = (uint32_t)min(m0 + 32 * wave + 2 * lane, p.m - 1) * 8u;
+        } else {
+            xg = uniform_ptr(static_cast<const char*>(p.x) + (size_t)k0 * 128);
+#pragma unroll
+            for (int j = 0; j < DA; ++j) {
+                const int u = (wave * DA + j) * 64 + lane, row = u >> 3, c = (u & 7) ^ ((row >> 1) & 7);
+                a_off[j] = (uint32_t)((int64_t)min(m0 + row, p.m - 1) * p.ldx * 2 + c * 16);
+            }
         }
         if constexpr (Q4K) {
             // rows past the window read its last row (their outputs are never stored)
@@ -175,7 +195,14 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
     };
     // load j < DA of this wave's share of activation stage s
     auto issue_a_piece = [&](int s, int j) __attribute__((always_inline)) {
-        lds_dma16(xg + (size_t)s * 128, a_off[j], lds0 + (s % 3) * C::ABuf + (wave * DA + j) * 1024);
+        if constexpr (I8) {
+            if (j < DA - 1)
+                lds_dma16(xg + (size_t)s * 64, a_off[j], lds0 + (s % 3) * C::ABuf + (wave * (DA - 1) + j) * 1024);
+            else if (lane < 16)
+                lds_dma16(sag + (size_t)s * p.m * 8, a_off[j], lds0 + (s % 3) * C::ABuf + C::BM * 64 + wave * 256);
+        } else {
+            lds_dma16(xg + (size_t)s * 128, a_off[j], lds0 + (s % 3) * C::ABuf + (wave * DA + j) * 1024);
+        }
     };
     auto issue_a = [&](int s) __attribute__((always_inline)) {
 #pragma unroll
@@ -472,8 +499,100 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
             general_epilogue(m0, n0);
     };
 
+    // ---- I8 (the INT8 mode): the reference's integer kernel, y = sum over 32-blocks b of (sa * d) * dot_b, with dot_b
+    // the exact int32 dot product of the block's int8 activation codes and weight codes. One v_mfma_i32_32x32x32_i8
+    // per block and accumulator tile takes the weight codes straight from the tiled layout (a lane's 16 bytes are
+    // codes 8 h .. 8 h + 7 and 16 + 8 h .. of row l % 32, h = l / 32) and the activation codes in the same order (the
+    // quantizer stores each block as codes 0..7, 16..23, 8..15, 24..31, so a lane reads 16 consecutive bytes); the
+    // int32 result is folded into the fp32 accumulator as fmaf(dot, sa * d, acc), block after block in k order (the
+    // order and the roundings of the row-major INT8 kernel). Stage s of three LDS buffers: wait for A(s), W(s);
+    // barrier; issue A(s + 2), W(s + 2) into the buffer stage s - 1 used; compute stage s. The fold (three VALU
+    // instructions per accumulator element and block) bounds the kernel, not the matrix cores.
+    auto compute_i8 = [&](int buf) __attribute__((always_inline)) {
+        const char* ab = smem + buf * C::ABuf;
+        const char* wb = smem + C::WBase + buf * C::WBuf + wave * C::WWave;
+        const int half = lane >> 5;
+        uint4 wc[CT][2], dwr[CT][4];
+        float2 sv[RT];
+#pragma unroll
+        for (int c = 0; c < CT; ++c) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b) wc[c][b] = *reinterpret_cast<const uint4*>(wb + c * 2048 + b * 1024 + 16 * lane);
+            // the fp16 scales (block 0 low, block 1 high) of accumulator rows 8 q + 4 h .. + 3
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                dwr[c][q] = *reinterpret_cast<const uint4*>(wb + CT * 2048 + c * 128 + 32 * q + 16 * half);
+        }
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) sv[rt] = *reinterpret_cast<const float2*>(ab + C::BM * 64 + (32 * rt + (lane & 31)) * 8);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            i32x4 xv[RT];
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const int row = 32 * rt + (lane & 31), chunk = (2 * b + half) ^ ((row >> 2) & 3);
+                xv[rt] = *reinterpret_cast<const i32x4*>(ab + row * 64 + 16 * chunk);
+            }
+            float dw[CT][16];
+#pragma unroll
+            for (int c = 0; c < CT; ++c)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const uint4 r4 = dwr[c][e >> 2];
+                    const uint32_t w = (e & 3) == 0 ? r4.x : (e & 3) == 1 ? r4.y : (e & 3) == 2 ? r4.z : r4.w;
+                    dw[c][e] = half_bits_to_float((uint16_t)(w >> (16 * b)));
+                }
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const float sa = b == 0 ? sv[rt].x : sv[rt].y;
+#pragma unroll
+                for (int c = 0; c < CT; ++c) {
+                    i32x16 zero;
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) zero[e] = 0;
+                    const i32x16 dot = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, wc[c][b]), xv[rt],
+                                                                              zero, 0, 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) acc[rt][c][e] = fmaf((float)dot[e], sa * dw[c][e], acc[rt][c][e]);
+                }
+            }
+        }
+    };
+    auto run_segment_i8 = [&](int m0, int n0, int k0, int S) __attribute__((always_inline)) {
+        start_tile(m0, n0, k0);
+        __syncthreads();  // every wave is done with the previous segment's LDS
+        issue_a(0);
+        issue_w(0);
+        if (S > 1) {
+            issue_a(1);
+            issue_w(1);
+        }
+#pragma unroll
+        for (int i = 0; i < RT; ++i)
+#pragma unroll
+            for (int j = 0; j < CT; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+        for (int s = 0; s < S; ++s) {
+            if (s + 1 < S)
+                wait_vm<DA + DW>();  // A(s), W(s) landed: A(s + 1), W(s + 1) may remain
+            else
+                wait_vm<0>();
+            __syncthreads();  // every wave's share of stage s is in LDS; every wave is done with stage s - 1
+            if (s + 2 < S) {
+                issue_a(s + 2);
+                issue_w(s + 2);
+            }
+            compute_i8(s % 3);
+        }
+    };
+
     // ---- one segment: stages k0 .. k0 + S - 1 of the tile at (m0, n0), accumulated from zero into acc
     auto run_segment = [&](int m0, int n0, int k0, int S) __attribute__((always_inline)) {
+        if constexpr (I8) {
+            run_segment_i8(m0, n0, k0, S);
+            return;
+        }
         start_tile(m0, n0, k0);
         __syncthreads();  // every wave is done with the previous segment's LDS
         issue_a(0);
@@ -669,10 +788,10 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
     }
 }
 
-template <typename T, int RT, int CT, int ACT, bool FAST, bool RES, bool SPLIT, bool Q4K = false>
+template <typename T, int RT, int CT, int ACT, bool FAST, bool RES, bool SPLIT, bool Q4K = false, bool I8 = false>
 __global__ __launch_bounds__(kWideThreads) void q8_wide_kernel(GemmParams p, WideSplit sp) {
-    __shared__ __attribute__((aligned(1024))) char smem[WideCfg<RT, CT, Q4K>::Lds];
-    wide_tiles<T, RT, CT, ACT, FAST, RES, SPLIT, Q4K>(p, sp, smem);
+    __shared__ __attribute__((aligned(1024))) char smem[WideCfg<RT, CT, Q4K, I8>::Lds];
+    wide_tiles<T, RT, CT, ACT, FAST, RES, SPLIT, Q4K, I8>(p, sp, smem);
 }
 
 // Two column ranges in one launch: 256 x 256 tiles on pa's columns, 128 x 256 tiles on pb's (the column split of
@@ -718,7 +837,7 @@ bool below_2gb(const GemmParams& p) {
     return y_end < INT32_MAX && (!p.res || r_end < INT32_MAX);
 }
 
-template <typename T, int RT, int CT, bool SPLIT, bool Q4K>
+template <typename T, int RT, int CT, bool SPLIT, bool Q4K, bool I8 = false>
 int launch_wide_s(GemmParams p, const WideSplit& sp, hipStream_t stream) {
     const dim3 grid(sp.G), block(kWideThreads);
     p.tiles_m = (p.m + 32 * RT - 1) / (32 * RT);
@@ -728,11 +847,12 @@ int launch_wide_s(GemmParams p, const WideSplit& sp, hipStream_t stream) {
                       (!p.bias || p.bias_dt == IDOLQ_F32) &&
                       (p.act == IDOLQ_ACT_NONE || p.act == IDOLQ_ACT_GELU_TANH || p.act == IDOLQ_ACT_RELU);
     if (!fast)
-        hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, IDOLQ_ACT_NONE, false, false, SPLIT, Q4K>), grid, block, 0, stream, p, sp);
+        hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, IDOLQ_ACT_NONE, false, false, SPLIT, Q4K, I8>), grid, block, 0, stream,
+                           p, sp);
     else
         with_fast_epilogue(p, [&](auto act, auto res) {
-            hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, decltype(act)::value, true, decltype(res)::value, SPLIT, Q4K>), grid,
-                               block, 0, stream, p, sp);
+            hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, decltype(act)::value, true, decltype(res)::value, SPLIT, Q4K, I8>),
+                               grid, block, 0, stream, p, sp);
         });
     return check_launch("q8_wide_kernel");
 }
@@ -762,7 +882,7 @@ int launch_wide_pair(GemmParams pa, GemmParams pb, int grid, hipStream_t stream,
 }
 
 // Workspace: tile counters in the first kCountBytes, then the partial tiles.
-constexpr size_t kCountBytes = 4096;
+constexpr size_t kCountBytes = kWideCountBytes;
 
 // The columns [n0, n0 + n) of a launch (multiples of 32). Q4K: p.groups counts weight rows (row-major blocks).
 template <bool Q4K>
@@ -780,6 +900,20 @@ GemmParams column_window(GemmParams p, int n0, int n) {
     p.y = static_cast<char*>(p.y) + (size_t)n0 * dtype_size(p.y_dt);
     p.n = n;
     return p;
+}
+
+// The stream-K split of the tiles left after whole rounds (tiles, S stages each, over cus workgroups; workspace: the
+// counters, then the partial tiles).
+WideSplit split_plan(long tiles, long S, long cus, void* workspace) {
+    const long dp = tiles / cus * cus, units = (tiles - dp) * S;
+    WideSplit sp{(int)cus, (int)dp, (int)(units / cus), (int)(units % cus),
+                 reinterpret_cast<float*>(static_cast<char*>(workspace) + kCountBytes), static_cast<int*>(workspace), 1, 8};
+    // in-phase ranges (all of L stages) on neighbouring tiles; groups of 4 row tiles when every tile is split (the
+    // walk of the whole tiles is then not involved)
+    const long g = std::gcd((long)sp.L, S), nsplit = tiles - dp;
+    if (sp.R == 0 && sp.L > 0 && sp.L / g > 1 && nsplit % (sp.L / g) == 0) sp.ph = (int)(sp.L / g);
+    if (dp == 0) sp.gh = 4;
+    return sp;
 }
 
 // Launch plans, costed in microseconds from MI355X measurements: a 64-deep stage of a round of tiles takes STAGE, a
@@ -848,21 +982,40 @@ int launch_wide_dtype(GemmParams p, void* workspace, size_t workspace_bytes, hip
     const WideShape& c = kShapes[best_shape];
     const long tiles = tiles_of(c);
     WideSplit sp = whole(tiles);
-    if (best_split) {
-        const long dp = tiles / cus * cus, units = (tiles - dp) * S;
-        sp = WideSplit{(int)cus, (int)dp, (int)(units / cus), (int)(units % cus),
-                       reinterpret_cast<float*>(static_cast<char*>(workspace) + kCountBytes), static_cast<int*>(workspace), 1, 8};
-        // in-phase ranges (all of L stages) on neighbouring tiles; groups of 4 row tiles when every tile is split
-        // (the walk of the whole tiles is then not involved)
-        const long g = std::gcd((long)sp.L, S), nsplit = tiles - dp;
-        if (sp.R == 0 && sp.L > 0 && sp.L / g > 1 && nsplit % (sp.L / g) == 0) sp.ph = (int)(sp.L / g);
-        if (dp == 0) sp.gh = 4;
-    }
+    if (best_split) sp = split_plan(tiles, S, cus, workspace);
     if (best_shape == 0) return launch_wide_s<T, 8, 2, false, Q4K>(p, sp, stream);
     return launch_shape<T, Q4K, 4, 2>(p, sp, best_split, stream);
 }
 
 }  // namespace
+
+// 4-element groups of y, the residual and the bias are vector-accessible
+void set_y_vec4(GemmParams& p) {
+    int vec4 = reinterpret_cast<uintptr_t>(p.y) % (4 * dtype_size(p.y_dt)) == 0 && p.ldy % 4 == 0;
+    if (p.res) vec4 = vec4 && reinterpret_cast<uintptr_t>(p.res) % (4 * dtype_size(p.res_dt)) == 0 && p.ldr % 4 == 0;
+    if (p.bias) vec4 = vec4 && reinterpret_cast<uintptr_t>(p.bias) % (4 * dtype_size(p.bias_dt)) == 0;
+    p.y_vec4 = vec4;
+}
+
+// The INT8 mode on tiled weights: 128 x 256 tiles (register budget of the fold), whole rounds or stream-K over the
+// tiles left after them, costed like the DEQUANT plans with the fold-bound stage time. p.qa / p.sa: the activation
+// codes and scales in the tiled quantizer's layout. The register epilogue takes bf16 outputs; others the general one.
+int launch_wide_i8(GemmParams p, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    constexpr double kStage = 2.0, kFixed = 9.0;
+    set_y_vec4(p);
+    const long cus = cu_count(), S = p.k / 64;
+    const long tiles = (long)((p.m + 127) / 128) * ((p.n + 255) / 256);
+    auto rounds = [&](long t) { return (t + cus - 1) / cus; };
+    const long dp = tiles / cus * cus, units = (tiles - dp) * S;
+    const size_t need = kCountBytes + (size_t)2 * cus * 128 * 256 * 4;
+    const double whole = rounds(tiles) * (S * kStage + kFixed);
+    const double split = (double)dp / cus * (S * kStage + kFixed) + (double)rounds(units) * kStage + 2 * kFixed + 6.0;
+    if (workspace && reinterpret_cast<uintptr_t>(workspace) % 256 == 0 && workspace_bytes >= need && units >= cus &&
+        split < whole)
+        return launch_wide_s<__bf16, 4, 2, true, false, true>(p, split_plan(tiles, S, cus, workspace), stream);
+    const WideSplit sp{(int)std::min(tiles, cus), 0, 0, 0, nullptr, nullptr, 1, 8};
+    return launch_wide_s<__bf16, 4, 2, false, false, true>(p, sp, stream);
+}
 
 bool wide_eligible(const GemmParams& p, int xt, int mode) {
     return mode == MODE_DEQUANT && (xt == XT_BF16 || xt == XT_F16) && p.w_tiled && p.x_aligned && p.k % 64 == 0 &&
@@ -877,11 +1030,7 @@ size_t wide_workspace_bytes() { return kCountBytes + (size_t)2 * cu_count() * 12
 namespace {
 template <bool Q4K>
 int launch_wide_any(GemmParams p, int xt, void* workspace, size_t workspace_bytes, hipStream_t stream) {
-    // 4-element groups of y, the residual and the bias are vector-accessible
-    int vec4 = reinterpret_cast<uintptr_t>(p.y) % (4 * dtype_size(p.y_dt)) == 0 && p.ldy % 4 == 0;
-    if (p.res) vec4 = vec4 && reinterpret_cast<uintptr_t>(p.res) % (4 * dtype_size(p.res_dt)) == 0 && p.ldr % 4 == 0;
-    if (p.bias) vec4 = vec4 && reinterpret_cast<uintptr_t>(p.bias) % (4 * dtype_size(p.bias_dt)) == 0;
-    p.y_vec4 = vec4;
+    set_y_vec4(p);
     if (workspace && reinterpret_cast<uintptr_t>(workspace) % 256 != 0) workspace = nullptr;
     if (xt == XT_BF16) return launch_wide_dtype<__bf16, Q4K>(p, workspace, workspace_bytes, stream);
     return launch_wide_dtype<_Float16, Q4K>(p, workspace, workspace_bytes, stream);

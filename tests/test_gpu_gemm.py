@@ -131,6 +131,68 @@ def test_exact_and_int8_modes_track_the_reference_kernels(m, n, k):
         assert norm_rel(yo, rounded(ref, dt)) < 1e-3
 
 
+@pytest.mark.parametrize("m,n_total,k,off,cnt,xdt", [
+    (256, 1024, 1024, 0, 1024, torch.float32),   # config 0's shape, fp32 activations (the reference's input)
+    (300, 520, 512, 32, 448, torch.bfloat16),    # ragged rows and a column window
+    (1, 96, 128, 0, 96, torch.float16),          # one row (the scale pairs past m), two stages
+    (512, 512, 4096, 0, 512, torch.bfloat16),    # stream-K (every tile split)
+    (4096, 1536, 6144, 0, 1536, torch.bfloat16), # the MLP block's down projection (stream-K)
+])
+def test_int8_on_tiled_weights_matches_the_row_major_int8_kernel(m, n_total, k, off, cnt, xdt):
+    # INT8 mode on tiled weights (int8 MFMA on the tiled fragments, the block scale fold in the wide kernel) against
+    # the row-major INT8 kernel on the same blocks: whole tiles give the same bits (the same int32 block dots, folded
+    # in the same order with the same roundings); with the tiles' k range split over the CUs the parts' sums differ
+    # only by fp32 reassociation, repeated calls are bit-identical, and every tile counter ends at zero. The small
+    # shapes also against the oracle's integer kernel (1e-5).
+    print(f"int8 tiled m={m} n={n_total} k={k} window {off}+{cnt} {xdt}", flush=True)
+    rng = np.random.default_rng(m + k)
+    a = rng.normal(0, 1, (m, k)).astype(np.float32)
+    wq = q8(rng, n_total, k)
+    b = rng.normal(0, 0.01, n_total).astype(np.float32)
+    x, wd, bt = to_dev(a).to(xdt), to_dev(wq), to_dev(b)
+    wt = L.tile_q8_0(wd, n_total, k)
+    kw = dict(bias=bt, mode=L.MODE_INT8, out_dtype=torch.float32)
+    raw = L.gemm(x, wd, n_total, off, cnt, **kw)
+    til = L.gemm(x, wt, n_total, off, cnt, tiled=True, **kw)
+    # an explicit workspace whose tile counters (after the codes and scales) start as garbage: the quantizer clears
+    # them, and the split GEMM leaves them at zero
+    lib = L.load()
+    full = int(lib.idolq_q8_0_gemm_workspace(m, k, L.MODE_INT8))
+    prefix = full - int(lib.idolq_q8_0_gemm_workspace(m, k, L.MODE_DEQUANT))
+    ws = torch.zeros(full, device=DEV, dtype=torch.uint8)
+    ws[prefix:prefix + 4096] = 7
+    spl = [L.gemm(x, wt, n_total, off, cnt, tiled=True, split=True, workspace=ws, **kw) for _ in range(2)]
+    torch.cuda.synchronize()
+    assert torch.equal(raw, til)
+    assert torch.equal(spl[0], spl[1])
+    assert norm_rel(spl[0].cpu().numpy(), til.cpu().numpy()) < 1e-6
+    assert int(ws[prefix:prefix + 4096].view(torch.int32).abs().sum().item()) == 0
+    if m * k <= 2 ** 20:
+        wrows = wq.reshape(n_total, -1)[off:off + cnt].reshape(-1)
+        ref = O.gemm_q8_int8(x.float().cpu().numpy(), wrows, cnt, k, b[off:off + cnt])
+        assert norm_rel(til.cpu().numpy(), ref) < 1e-5
+
+
+def test_int8_on_tiled_weights_register_epilogue():
+    # bf16 output through the register epilogue (bias, residual aliasing y, tanh-GELU), whole tiles and split: the
+    # same bits as the row-major INT8 kernel's epilogue for whole tiles, within the output rounding when split
+    rng = np.random.default_rng(31)
+    m, n, k = 1000, 768, 2048
+    x = to_dev(rng.normal(0, 1, (m, k)).astype(np.float32)).bfloat16()
+    wq = to_dev(q8(rng, n, k))
+    wt = L.tile_q8_0(wq, n, k)
+    bt = to_dev(rng.normal(0, 0.1, n).astype(np.float32))
+    res = to_dev(rng.normal(0, 1, (m, n)).astype(np.float32)).bfloat16()
+    outs = []
+    for w, tiled, split in ((wq, False, False), (wt, True, False), (wt, True, True)):
+        y = res.clone()
+        L.gemm(x, w, n, bias=bt, residual=y, act=L.ACT_GELU_TANH, mode=L.MODE_INT8, out=y, tiled=tiled, split=split)
+        outs.append(y)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    assert norm_rel(outs[2].float().cpu().numpy(), outs[0].float().cpu().numpy()) < 1e-2
+
+
 def test_epilogue_window_residual_alias_and_activations():
     rng = np.random.default_rng(15)
     m, n, k = 67, 160, 256
