@@ -963,7 +963,7 @@ extern "C" int idolq_q8_0_gemm_noalloc(const void* x, int x_dtype, int64_t m, in
         // GEMM's own checks handle bad shapes and empty inputs)
         return idolq_q8_0_gemm(x, x_dtype, m, k, ldx, w, n_total, n_offset, n, bias, bias_dtype, residual,
                                residual_dtype, ldr, act, mode, flags, y, y_dtype, ldy, nullptr, 0, stream);
-    const size_t need = idolq_q8_0_gemm_workspace(m, k, eff);
+    const size_t need = int8_prefix_bytes(m, k);  // the codes and scales (tiled weights then run whole tiles)
     if (need > kNoAllocScratchBytes)
         return fail(IDOLQ_EINVAL, "INT8 GEMM of m x k = " + std::to_string(m) + " x " + std::to_string(k) + " needs " +
                                       std::to_string(need) + " bytes of scratch; idolq_q8_0_gemm_noalloc holds " +

@@ -44,13 +44,15 @@ enum {
  *   EXACT    codes fed to bf16/fp16 MFMA exactly, each 32-deep block summed in fp32 and scaled by its fp32 d; fp32
  *            activations are split into bf16 high and low parts. Tracks the reference's CPU float kernel.
  *   INT8     activations quantized per row and 32-block to int8 exactly as the reference's integer kernel does,
- *            int8 MFMA with int32 block sums, scales folded per block in fp32. Needs a workspace.
+ *            int8 MFMA with int32 block sums, scales folded per block in fp32. Needs a workspace. On tiled weights
+ *            the same bits as on row-major weights when tiles are not split along k.
  *   AUTO     DEQUANT for bf16/fp16 activations, EXACT for fp32. */
 enum { IDOLQ_MODE_AUTO = 0, IDOLQ_MODE_DEQUANT = 1, IDOLQ_MODE_EXACT = 2, IDOLQ_MODE_INT8 = 3 };
 
 /* GEMM flags. ROUND_BEFORE_BIAS rounds the product to the output dtype before the bias is added, as the reference's
  * fused GPU path does (tools/idol_triton.py:84-89). TILED_WEIGHTS: w is in the tiled Q8_0 layout written by
- * idolq_q8_0_tile (DEQUANT mode, bf16/fp16 activations with 16-byte aligned rows, k % 64 == 0, n_offset % 32 == 0). */
+ * idolq_q8_0_tile (DEQUANT mode with bf16/fp16 activations, or INT8 mode; activation rows 16-byte aligned,
+ * k % 64 == 0, n_offset % 32 == 0). */
 enum { IDOLQ_FLAG_ROUND_BEFORE_BIAS = 1, IDOLQ_FLAG_TILED_WEIGHTS = 2 };
 
 enum {
@@ -78,7 +80,9 @@ int64_t idolq_q8_0_bytes(int64_t n, int64_t k);
  *   act      IDOLQ_ACT_*, applied after bias and residual
  *   y        [m x n] in y_dtype, row stride ldy
  *   workspace / workspace_bytes  scratch of idolq_q8_0_gemm_workspace bytes: required by IDOLQ_MODE_INT8 (quantized
- *            activations); optional for IDOLQ_MODE_DEQUANT with tiled weights, where it lets the k stages of the
+ *            activations and scales, m * k * 9 / 8 bytes and some padding at the start; with tiled weights the
+ *            rest, when present, is used like the DEQUANT workspace and needs no zero-fill: the call clears its
+ *            counters); optional for IDOLQ_MODE_DEQUANT with tiled weights, where it lets the k stages of the
  *            tiles left after whole rounds of the CUs be split over the CUs (tile counters, then partial tiles). A
  *            DEQUANT workspace must be zero-filled before its first use and used by one stream at a time; calls
  *            leave its counters at zero, ready for the next call.
@@ -89,9 +93,9 @@ int idolq_q8_0_gemm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ld
                     int residual_dtype, int64_t ldr, int act, int mode, int flags, void* y, int y_dtype, int64_t ldy,
                     void* workspace, size_t workspace_bytes, void* stream);
 
-/* Workspace bytes idolq_q8_0_gemm uses for m rows of depth k in the given mode: the quantized activations for
- * IDOLQ_MODE_INT8, the tile counters and partial tiles of the current device's CUs for IDOLQ_MODE_DEQUANT, 0 for
- * IDOLQ_MODE_EXACT. */
+/* Workspace bytes idolq_q8_0_gemm uses for m rows of depth k in the given mode: the quantized activations and
+ * scales, then room for the tiled path's split, for IDOLQ_MODE_INT8; the tile counters and partial tiles of the
+ * current device's CUs for IDOLQ_MODE_DEQUANT; 0 for IDOLQ_MODE_EXACT. */
 size_t idolq_q8_0_gemm_workspace(int64_t m, int64_t k, int mode);
 
 /* idolq_q8_0_gemm for callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses

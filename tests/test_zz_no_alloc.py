@@ -14,12 +14,12 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
 
 
-def _call_noalloc(x, w, n_total, n, bias, mode, out):
+def _call_noalloc(x, w, n_total, n, bias, mode, out, flags=0):
     lib = L.load()
     m, k = x.shape
     return lib.idolq_q8_0_gemm_noalloc(
         ctypes.c_void_p(x.data_ptr()), L.DTYPE_CODE[x.dtype], m, k, x.stride(0), ctypes.c_void_p(w.data_ptr()),
-        n_total, 0, n, ctypes.c_void_p(bias.data_ptr()), L.F32, None, 0, 0, L.ACT_GELU_ERF, mode, 0,
+        n_total, 0, n, ctypes.c_void_p(bias.data_ptr()), L.F32, None, 0, 0, L.ACT_GELU_ERF, mode, flags,
         ctypes.c_void_p(out.data_ptr()), L.DTYPE_CODE[out.dtype], out.stride(0),
         ctypes.c_void_p(torch.cuda.current_stream(DEV).cuda_stream))
 
@@ -37,6 +37,22 @@ def test_noalloc_gemm_matches_the_workspace_gemm(mode):
         want = L.gemm(x, w, n, bias=b, act=L.ACT_GELU_ERF, mode=mode, out_dtype=torch.float32)
         got = torch.full((m, n), float("nan"), device=DEV)
         assert _call_noalloc(x, w, n, n, b, mode, got) == 0, L.load().idolq_last_error()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), (m, n, k)
+
+
+def test_noalloc_int8_on_tiled_weights_matches_the_workspace_gemm():
+    # INT8 on tiled weights takes its codes and scales from the array too (whole tiles): the same bits as the
+    # workspace call without split, on two calls in a row, the second smaller
+    rng = np.random.default_rng(47)
+    for m, n, k in ((1024, 768, 2048), (300, 224, 512)):
+        x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(DEV).bfloat16()
+        w = torch.from_numpy(O.q8_0_quantize(rng.normal(0, 0.02, (n, k)).astype(np.float32))).to(DEV)
+        wt = L.tile_q8_0(w, n, k)
+        b = torch.from_numpy(rng.normal(0, 0.01, n).astype(np.float32)).to(DEV)
+        want = L.gemm(x, wt, n, bias=b, act=L.ACT_GELU_ERF, mode=L.MODE_INT8, out_dtype=torch.float32, tiled=True)
+        got = torch.full((m, n), float("nan"), device=DEV)
+        assert _call_noalloc(x, wt, n, n, b, L.MODE_INT8, got, L.FLAG_TILED_WEIGHTS) == 0, L.load().idolq_last_error()
         torch.cuda.synchronize()
         assert torch.equal(got, want), (m, n, k)
 
