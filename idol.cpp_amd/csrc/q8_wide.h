@@ -732,7 +732,7 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
                     // in kH passes of kP uint4 pieces (register budget); in a pass every stored part is read with
                     // one batch of loads (one round trip per part): the parts before this one are summed into t,
                     // then this part's own pieces are added to t, then the parts after it.
-                    constexpr int kH = RT >= 8 ? 4 : 2, kP = kQ / kH;
+                    constexpr int kH = RT >= 8 || I8 ? 4 : 2, kP = kQ / kH;  // I8: within 256 VGPRs
                     auto slot_off = [&](int c) __attribute__((always_inline)) {
                         return (2 * c + (t0 > begin_of(c) ? 1 : 0)) * kSlot + tid * 16;
                     };
