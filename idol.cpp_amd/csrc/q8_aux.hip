@@ -171,6 +171,46 @@ __global__ __launch_bounds__(256) void quantize_act16_kernel(const T* __restrict
     }
 }
 
+// The EXACT mode on tiled weights: activations (fp32, bf16 or fp16, 16-byte aligned rows) to bf16 high parts
+// hi = bf16(x) and low parts lo = bf16(x - hi), [m, k] each with row stride k (the split of the row-major EXACT
+// kernel), eight values per thread; zero: nzero ints cleared on the side (the GEMM's tile counters).
+template <typename T>
+__global__ __launch_bounds__(256) void split_bf16_kernel(const T* __restrict__ x, int64_t m, int64_t k, int64_t ldx,
+                                                         uint16_t* __restrict__ hi, uint16_t* __restrict__ lo,
+                                                         int* __restrict__ zero, int nzero) {
+    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (zero)
+        for (int64_t i = id; i < nzero; i += (int64_t)gridDim.x * blockDim.x) zero[i] = 0;
+    const int64_t per_row = k / 8;
+    if (id >= m * per_row) return;
+    const int64_t r = id / per_row, c = (id - r * per_row) * 8;
+    float v[8];
+    if constexpr (std::is_same<T, float>::value) {
+        const float4 a = *reinterpret_cast<const float4*>(x + r * ldx + c);
+        const float4 b = *reinterpret_cast<const float4*>(x + r * ldx + c + 4);
+        v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+    } else {
+        const uint4 raw = *reinterpret_cast<const uint4*>(x + r * ldx + c);
+        const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint16_t h = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+            v[e] = std::is_same<T, __bf16>::value ? bf16_bits_to_float(h) : half_bits_to_float(h);
+        }
+    }
+    uint32_t h2[4], l2[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const uint16_t h0 = float_to_bf16_bits(v[2 * e]), h1 = float_to_bf16_bits(v[2 * e + 1]);
+        const uint16_t l0 = float_to_bf16_bits(v[2 * e] - bf16_bits_to_float(h0));
+        const uint16_t l1 = float_to_bf16_bits(v[2 * e + 1] - bf16_bits_to_float(h1));
+        h2[e] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+        l2[e] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+    }
+    *reinterpret_cast<uint4*>(hi + r * k + c) = make_uint4(h2[0], h2[1], h2[2], h2[3]);
+    *reinterpret_cast<uint4*>(lo + r * k + c) = make_uint4(l2[0], l2[1], l2[2], l2[3]);
+}
+
 // ------------------------------------------------------------------------------------------------ elementwise
 __global__ __launch_bounds__(256) void activation_kernel(void* x, int dt, int64_t count, int act) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -247,6 +287,24 @@ unsigned grid_for(int64_t items, int threads = 256) {
 }
 
 }  // namespace
+
+// The high / low split of the EXACT mode on tiled weights (split_bf16_kernel); k % 8 == 0, aligned rows.
+int split_bf16_launch(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, uint16_t* hi, uint16_t* lo,
+                      int* zero, int nzero, hipStream_t stream) {
+    const int64_t n = m * (k / 8);
+    if (n == 0) return IDOLQ_OK;
+    const dim3 grid((unsigned)((n + 255) / 256));
+    if (x_dtype == IDOLQ_BF16)
+        hipLaunchKernelGGL(split_bf16_kernel<__bf16>, grid, dim3(256), 0, stream, static_cast<const __bf16*>(x), m, k,
+                           ldx, hi, lo, zero, nzero);
+    else if (x_dtype == IDOLQ_F16)
+        hipLaunchKernelGGL(split_bf16_kernel<_Float16>, grid, dim3(256), 0, stream, static_cast<const _Float16*>(x), m,
+                           k, ldx, hi, lo, zero, nzero);
+    else
+        hipLaunchKernelGGL(split_bf16_kernel<float>, grid, dim3(256), 0, stream, static_cast<const float*>(x), m, k, ldx,
+                           hi, lo, zero, nzero);
+    return check_launch("split_bf16_kernel");
+}
 
 // The tiled-GEMM layout of the INT8 mode (quantize_act16_kernel<T, true>): x rows 16-byte aligned, k a multiple of 64.
 int quantize_act_tiled_launch(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, int8_t* qa, float* scale,

@@ -31,6 +31,7 @@ struct GemmParams {
     int y_vec4;     // y, the residual and the bias allow vector access to 4-element groups
     // INT8 mode
     const int8_t* qa;
+    const void* x_lo;  // EXACT on tiled weights: the bf16 low parts of fp32 activations (p.x: the high parts)
     const float* sa;
     int32_t* dots;
 };
@@ -66,6 +67,8 @@ constexpr size_t kWideCountBytes = 4096;  // the tile counters at the start of t
 int launch_wide(GemmParams p, int xt, void* workspace, size_t workspace_bytes, hipStream_t stream);
 // The INT8 mode on tiled weights (p.qa, p.sa from the tiled quantizer); workspace as launch_wide's (may be null).
 int launch_wide_i8(GemmParams p, void* workspace, size_t workspace_bytes, hipStream_t stream);
+// The EXACT mode on tiled weights (p.x, p.x_lo: bf16 high and low parts of the activations, row stride k).
+int launch_wide_exact(GemmParams p, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 // The small-m form (q8_gemv.hip): m <= kGemvMaxRows activation rows on GGUF row-major weights (k % 256 == 0, 16-byte
 // aligned), DEQUANT on 16-bit activations or EXACT; 16 weight rows per workgroup, the depth split over 8 waves.

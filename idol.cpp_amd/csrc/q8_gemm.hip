@@ -780,6 +780,9 @@ int quantize_act_launch(const void* x, int x_dtype, int64_t m, int64_t k, int64_
                         int32_t* qsum, hipStream_t stream);
 int quantize_act_tiled_launch(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, int8_t* qa, float* scale,
                               int* zero, int nzero, hipStream_t stream);
+// Splits activations into bf16 high and low parts for the EXACT mode on tiled weights (q8_aux.hip).
+int split_bf16_launch(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, uint16_t* hi, uint16_t* lo,
+                      int* zero, int nzero, hipStream_t stream);
 
 // INT8 scratch: the activation codes (m x k bytes), then the scales (m x k / 32 fp32, 16 bytes of padding), each
 // rounded up to 256 bytes; the tiled path may use the rest as the stream-K workspace.
@@ -789,14 +792,21 @@ size_t int8_prefix_bytes(int64_t m, int64_t k) {
     return qa + sa;
 }
 
+// Scratch of the EXACT mode on tiled weights: the bf16 high parts, then the low parts (m x k x 2 bytes each, rounded
+// up to 256 bytes); the rest may be the stream-K workspace.
+size_t exact_prefix_bytes(int64_t m, int64_t k) { return 2 * (((size_t)m * (size_t)k * 2 + 255) / 256 * 256); }
+
 }  // namespace idolq
 
 using namespace idolq;
 
 extern "C" size_t idolq_q8_0_gemm_workspace(int64_t m, int64_t k, int mode) {
     if (mode == IDOLQ_MODE_DEQUANT) return wide_workspace_bytes();
-    if (mode != IDOLQ_MODE_INT8 || m <= 0 || k <= 0 || k % kQ8Block) return 0;
-    // the scratch of either INT8 path, plus the stream-K workspace the tiled path can use after it
+    if (m <= 0 || k <= 0 || k % kQ8Block) return 0;
+    // EXACT: the scratch of the tiled path (the row-major EXACT kernel needs none), INT8: the scratch of either
+    // path; each plus the stream-K workspace the tiled path can use after it
+    if (mode == IDOLQ_MODE_EXACT) return exact_prefix_bytes(m, k) + wide_workspace_bytes();
+    if (mode != IDOLQ_MODE_INT8) return 0;
     return int8_prefix_bytes(m, k) + wide_workspace_bytes();
 }
 
@@ -824,8 +834,8 @@ extern "C" int idolq_q8_0_gemm(const void* x, int x_dtype, int64_t m, int64_t k,
     if (mode == IDOLQ_MODE_DEQUANT && x_dtype == IDOLQ_F32)
         return fail(IDOLQ_EINVAL, "DEQUANT mode takes bf16 or fp16 activations");
     const bool tiled = (flags & IDOLQ_FLAG_TILED_WEIGHTS) != 0;
-    if (tiled && (mode == IDOLQ_MODE_EXACT || k % 64 || n_offset % 32))
-        return fail(IDOLQ_EINVAL, "tiled weights need DEQUANT or INT8 mode, k a multiple of 64 and n_offset a multiple of 32");
+    if (tiled && (k % 64 || n_offset % 32))
+        return fail(IDOLQ_EINVAL, "tiled weights need k a multiple of 64 and n_offset a multiple of 32");
     if (m == 0 || n == 0) return IDOLQ_OK;  // empty input: nothing to read or write (pointers may be null)
     if (!x || !w || !y) return fail(IDOLQ_EINVAL, "x, w and y must be non-null");
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -887,6 +897,29 @@ extern "C" int idolq_q8_0_gemm(const void* x, int x_dtype, int64_t m, int64_t k,
         p.qa = qa;
         p.sa = sa;
         return launch_int8<128, 128, false>(p, w4, s);
+    }
+    if (mode == IDOLQ_MODE_EXACT && tiled) {
+        // x -> bf16 high and low parts (x - hi rounded to bf16) in the scratch, then two bf16 products per block
+        const size_t need = exact_prefix_bytes(m, k);
+        if (!workspace || workspace_bytes < need)
+            return fail(IDOLQ_EINVAL, "EXACT mode on tiled weights needs a workspace of idolq_q8_0_gemm_workspace() bytes");
+        if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return fail(IDOLQ_EINVAL, "workspace must be 16-byte aligned");
+        const size_t xsz = dtype_size(x_dtype);
+        if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || ((size_t)ldx * xsz) % 16 != 0 || (reinterpret_cast<uintptr_t>(w) & 15) != 0)
+            return fail(IDOLQ_EINVAL, "the tiled EXACT GEMM needs 16-byte aligned activation rows and weights");
+        if (p.groups <= 0) return fail(IDOLQ_EINVAL, "tiled weights: n_total exceeds the layout");
+        uint16_t* hi = static_cast<uint16_t*>(workspace);
+        uint16_t* lo = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + need / 2);
+        char* rest = static_cast<char*>(workspace) + need;
+        const bool has_rest = workspace_bytes >= need + wide_workspace_bytes();
+        int rc = split_bf16_launch(x, x_dtype, m, k, ldx, hi, lo, has_rest ? reinterpret_cast<int*>(rest) : nullptr,
+                                   has_rest ? (int)(kWideCountBytes / sizeof(int)) : 0, s);
+        if (rc) return rc;
+        p.x = hi;
+        p.x_lo = lo;
+        p.ldx = k;
+        p.x_aligned = true;
+        return launch_wide_exact(p, has_rest ? rest : nullptr, has_rest ? workspace_bytes - need : 0, s);
     }
     const int xt = x_dtype == IDOLQ_BF16 ? XT_BF16 : x_dtype == IDOLQ_F16 ? XT_F16 : XT_F32;
     const int kmode = mode == IDOLQ_MODE_DEQUANT ? MODE_DEQUANT : MODE_EXACT;
@@ -958,19 +991,24 @@ extern "C" int idolq_q8_0_gemm_noalloc(const void* x, int x_dtype, int64_t m, in
                                        const void* residual, int residual_dtype, int64_t ldr, int act, int mode,
                                        int flags, void* y, int y_dtype, int64_t ldy, void* stream) {
     const int eff = mode == IDOLQ_MODE_AUTO ? (x_dtype == IDOLQ_F32 ? IDOLQ_MODE_EXACT : IDOLQ_MODE_DEQUANT) : mode;
-    if (eff != IDOLQ_MODE_INT8 || m <= 0 || n <= 0 || k <= 0 || k % kQ8Block)
-        // DEQUANT without a workspace runs whole tiles and EXACT needs none: nothing to take from the scratch (the
-        // GEMM's own checks handle bad shapes and empty inputs)
+    const bool tiled = (flags & IDOLQ_FLAG_TILED_WEIGHTS) != 0;
+    if (!(eff == IDOLQ_MODE_INT8 || (eff == IDOLQ_MODE_EXACT && tiled)) || m <= 0 || n <= 0 || k <= 0 || k % kQ8Block)
+        // DEQUANT without a workspace runs whole tiles and row-major EXACT needs none: nothing to take from the
+        // scratch (the GEMM's own checks handle bad shapes and empty inputs)
         return idolq_q8_0_gemm(x, x_dtype, m, k, ldx, w, n_total, n_offset, n, bias, bias_dtype, residual,
                                residual_dtype, ldr, act, mode, flags, y, y_dtype, ldy, nullptr, 0, stream);
-    const size_t need = int8_prefix_bytes(m, k);  // the codes and scales (tiled weights then run whole tiles)
+    // INT8: the codes and scales, EXACT on tiled weights: the high and low parts (tiled weights then run whole tiles)
+    const size_t need = eff == IDOLQ_MODE_INT8 ? int8_prefix_bytes(m, k) : exact_prefix_bytes(m, k);
     if (need > kNoAllocScratchBytes)
-        return fail(IDOLQ_EINVAL, "INT8 GEMM of m x k = " + std::to_string(m) + " x " + std::to_string(k) + " needs " +
-                                      std::to_string(need) + " bytes of scratch; idolq_q8_0_gemm_noalloc holds " +
-                                      std::to_string(kNoAllocScratchBytes) + " (m * k * 9 / 8 bytes at most)");
+        return fail(IDOLQ_EINVAL, std::string(eff == IDOLQ_MODE_INT8 ? "INT8" : "EXACT") + " GEMM of m x k = " +
+                                      std::to_string(m) + " x " + std::to_string(k) + " needs " + std::to_string(need) +
+                                      " bytes of scratch; idolq_q8_0_gemm_noalloc holds " +
+                                      std::to_string(kNoAllocScratchBytes) +
+                                      " (INT8: m * k * 9 / 8 bytes at most, EXACT on tiled weights: m * k * 4)");
     int rc = IDOLQ_OK;
     void* ptr = noalloc_scratch(&rc);
     if (!ptr) return rc;
+    // exactly the scratch: no stream-K room, so every call runs whole tiles
     return idolq_q8_0_gemm(x, x_dtype, m, k, ldx, w, n_total, n_offset, n, bias, bias_dtype, residual, residual_dtype,
-                           ldr, act, mode, flags, y, y_dtype, ldy, ptr, kNoAllocScratchBytes, stream);
+                           ldr, act, mode, flags, y, y_dtype, ldy, ptr, need, stream);
 }

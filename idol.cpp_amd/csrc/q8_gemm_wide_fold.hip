@@ -1,0 +1,45 @@
+// The modes that fold 32-block sums on tiled weights (q8_wide.h, FOLD): INT8 (int8 MFMA on the tiled fragments,
+// fmaf(dot, sa * d, acc)) and EXACT (exact codes against the bf16 high and low parts of fp32 activations,
+// fmaf(sum, d, acc)). Built with MFMA results in VGPRs: the fold reads every result element with the vector ALU, and
+// results in AGPRs would cost a copy per element.
+#include "q8_wide.h"
+
+#include <algorithm>
+
+namespace idolq {
+
+namespace {
+
+// 128 x 256 tiles (the fold's register budget), whole rounds or stream-K over the tiles left after them, costed like
+// the DEQUANT plans with the mode's stage time. The register epilogue takes bf16 outputs; others the general one.
+template <int FOLD>
+int launch_wide_fold(GemmParams p, double stage, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    constexpr double kFixed = 9.0;
+    set_y_vec4(p);
+    const long cus = cu_count(), S = p.k / 64;
+    const long tiles = (long)((p.m + 127) / 128) * ((p.n + 255) / 256);
+    auto rounds = [&](long t) { return (t + cus - 1) / cus; };
+    const long dp = tiles / cus * cus, units = (tiles - dp) * S;
+    const size_t need = kCountBytes + (size_t)2 * cus * 128 * 256 * 4;
+    const double whole = rounds(tiles) * (S * stage + kFixed);
+    const double split = (double)dp / cus * (S * stage + kFixed) + (double)rounds(units) * stage + 2 * kFixed + 6.0;
+    if (workspace && reinterpret_cast<uintptr_t>(workspace) % 256 == 0 && workspace_bytes >= need && units >= cus &&
+        split < whole)
+        return launch_wide_s<__bf16, 4, 2, true, false, FOLD>(p, split_plan(tiles, S, cus, workspace), stream);
+    const WideSplit sp{(int)std::min(tiles, cus), 0, 0, 0, nullptr, nullptr, 1, 8};
+    return launch_wide_s<__bf16, 4, 2, false, false, FOLD>(p, sp, stream);
+}
+
+}  // namespace
+
+// p.qa / p.sa: the activation codes and scales in the tiled quantizer's layout (fold-bound: ~2 us per stage)
+int launch_wide_i8(GemmParams p, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    return launch_wide_fold<kFoldI8>(p, 2.0, workspace, workspace_bytes, stream);
+}
+
+// p.x / p.x_lo: the bf16 high and low parts of the activations, row stride k (MFMA-bound: twice DEQUANT's products)
+int launch_wide_exact(GemmParams p, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    return launch_wide_fold<kFoldExact>(p, 1.9, workspace, workspace_bytes, stream);
+}
+
+}  // namespace idolq

@@ -83,19 +83,25 @@ struct WideSplit {
 // super-block (j = stage % 4), whose codes are the low and the high nibbles of the same 32 bytes 16 + 32 j .. of the
 // block. Per 32-row group and stage a wave loads those 32 bytes of each row (1 KB, lane l: row l % 32, bytes
 // 16 (l / 32) .. + 15) and the rows' 16-byte headers (512 bytes), straight from the row-major bytes.
-// I8 (the INT8 mode): a stage of activations is BM rows x 64 int8 codes, then the rows' two fp32 block scales.
-template <int RT, int CT, bool Q4K = false, bool I8 = false>
+// FOLD: 0 (DEQUANT: one accumulation over the whole depth), kFoldI8 (the INT8 mode: a stage of activations is BM
+// rows x 64 int8 codes, then the rows' two fp32 block scales), kFoldExact (the EXACT mode: BM rows x 64 bf16 high
+// parts, then BM rows x 64 bf16 low parts of fp32 activations).
+constexpr int kFoldI8 = 1, kFoldExact = 2;
+template <int RT, int CT, bool Q4K = false, int FOLD = 0>
 struct WideCfg {
+    static constexpr bool I8 = FOLD == kFoldI8, EX = FOLD == kFoldExact;
     static constexpr int BM = 32 * RT, BN = 128 * CT;
-    static constexpr int ABuf = I8 ? BM * 72 : BM * 128;  // one stage of activations: BM rows x 64 16-bit values
+    // one stage of activations: BM rows x 64 16-bit values
+    static constexpr int ABuf = I8 ? BM * 72 : EX ? BM * 256 : BM * 128;
     static constexpr int WCode = Q4K ? 1024 : 2048;  // one 32-row group's codes per stage
     static constexpr int WScale = Q4K ? 512 : 128;   // and its scales (Q4_K: the super-block headers)
     static constexpr int WWave = CT * (WCode + WScale);  // one stage of one wave's weight groups: codes, then scales
     static constexpr int WBuf = 4 * WWave;
     static constexpr int WBase = 3 * ABuf;
     static constexpr int Lds = WBase + 3 * WBuf;
-    // activation loads per wave per stage: 1 KB each; I8: BM / 64 of 1 KB and one of the rows' scales (256 bytes)
-    static constexpr int DA = I8 ? BM / 64 + 1 : BM / 32;
+    // activation loads per wave per stage: 1 KB each; I8: BM / 64 of 1 KB and one of the rows' scales (256 bytes);
+    // EX: BM / 32 of the high parts, then as many of the low parts
+    static constexpr int DA = I8 ? BM / 64 + 1 : EX ? BM / 16 : BM / 32;
     static constexpr int DW = Q4K ? 2 * CT : 2 * CT + 1;  // weight loads per wave per stage
     static_assert(Lds <= 163840, "LDS budget");
 };
@@ -136,10 +142,11 @@ __device__ __forceinline__ void q4k_header(uint4 hd, int pair, float (&ab)[4]) {
 
 // The tiles of one launch shape (RT, CT), with this workgroup's share of them; smem: the kernel's LDS (C::Lds bytes).
 // FAST selects the register epilogue (activation ACT, a residual iff RES), otherwise the general one.
-// I8: the INT8 mode (see run_segment_i8); T then only names the output type of the register epilogue.
-template <typename T, int RT, int CT, int ACT, bool FAST, bool RES, bool SPLIT, bool Q4K, bool I8 = false>
+// FOLD: the INT8 or EXACT mode (see run_segment_fold); T then only names the output type of the register epilogue.
+template <typename T, int RT, int CT, int ACT, bool FAST, bool RES, bool SPLIT, bool Q4K, int FOLD = 0>
 __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit& sp, char* smem) {
-    typedef WideCfg<RT, CT, Q4K, I8> C;
+    typedef WideCfg<RT, CT, Q4K, FOLD> C;
+    constexpr bool I8 = C::I8, EX = C::EX;
     typedef typename PipeMfma<T>::vec Vec;
     typedef typename PipeMfma<T>::pair T2;
     constexpr int DA = C::DA, DW = C::DW;
@@ -151,7 +158,7 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
     const uint32_t lds0 = (uint32_t)(size_t)(lds_char*)smem;
     const char* xg;  // activations and weights of the segment's first stage
     const char* wg;
-    const char* sag = nullptr;  // I8: the activation scales of the segment's first stage
+    const char* sag = nullptr;  // I8: the activation scales of the segment's first stage; EX: the low parts
 
     // ---- per-tile load offsets (bytes, 32-bit)
     // activations: load j of this wave fills LDS 16-byte chunks u = 64 (DA wave + j) + lane of the stage buffer:
@@ -176,10 +183,13 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
             // onward (the scale buffer is padded by 16 bytes), feeding only outputs that are never stored
             a_off[DA - 1] = (uint32_t)min(m0 + 32 * wave + 2 * lane, p.m - 1) * 8u;
         } else {
+            // EX: the low parts share the high parts' layout (row stride k), so their loads use the same offsets
+            constexpr int DX = EX ? DA / 2 : DA;
             xg = uniform_ptr(static_cast<const char*>(p.x) + (size_t)k0 * 128);
+            if constexpr (EX) sag = uniform_ptr(static_cast<const char*>(p.x_lo) + (size_t)k0 * 128);
 #pragma unroll
-            for (int j = 0; j < DA; ++j) {
-                const int u = (wave * DA + j) * 64 + lane, row = u >> 3, c = (u & 7) ^ ((row >> 1) & 7);
+            for (int j = 0; j < DX; ++j) {
+                const int u = (wave * DX + j) * 64 + lane, row = u >> 3, c = (u & 7) ^ ((row >> 1) & 7);
                 a_off[j] = (uint32_t)((int64_t)min(m0 + row, p.m - 1) * p.ldx * 2 + c * 16);
             }
         }
@@ -206,6 +216,12 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
                 lds_dma16(xg + (size_t)s * 64, a_off[j], lds0 + (s % 3) * C::ABuf + (wave * (DA - 1) + j) * 1024);
             else if (lane < 16)
                 lds_dma16(sag + (size_t)s * p.m * 8, a_off[j], lds0 + (s % 3) * C::ABuf + C::BM * 64 + wave * 256);
+        } else if constexpr (EX) {
+            constexpr int DX = DA / 2;
+            if (j < DX)
+                lds_dma16(xg + (size_t)s * 128, a_off[j], lds0 + (s % 3) * C::ABuf + (wave * DX + j) * 1024);
+            else
+                lds_dma16(sag + (size_t)s * 128, a_off[j - DX], lds0 + (s % 3) * C::ABuf + C::BM * 128 + (wave * DX + j - DX) * 1024);
         } else {
             lds_dma16(xg + (size_t)s * 128, a_off[j], lds0 + (s % 3) * C::ABuf + (wave * DA + j) * 1024);
         }
@@ -560,7 +576,74 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
             }
         }
     };
-    auto run_segment_i8 = [&](int m0, int n0, int k0, int S) __attribute__((always_inline)) {
+    // ---- EX (the EXACT mode): the reference's float kernel, y = sum over 32-blocks b of d * s_b, with s_b the fp32
+    // sum of the block's products of fp32 activations and exact codes. The activations come as bf16 high and low
+    // parts (x = hi + lo to within 2^-16 relative); per block and accumulator tile four v_mfma_f32_32x32x16_bf16
+    // (the high parts' two 16-deep steps, then the low parts') sum into a fresh fp32 tile that is folded as
+    // fmaf(s, d, acc), block after block: the operations and order of the row-major EXACT kernel.
+    auto codes_bf16 = [&](uint32_t lo, uint32_t hi) __attribute__((always_inline)) {
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t word = e < 2 ? lo : hi;
+            const int sh = 16 * (e & 1);
+            const f32x2 f = {(float)(int)(int8_t)(uint8_t)(word >> sh), (float)(int)(int8_t)(uint8_t)(word >> (sh + 8))};
+            o[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+        }
+        return __builtin_bit_cast(bf16x8, make_uint4(o[0], o[1], o[2], o[3]));
+    };
+    auto compute_ex = [&](int buf) __attribute__((always_inline)) {
+        const char* ab = smem + buf * C::ABuf;
+        const char* wb = smem + C::WBase + buf * C::WBuf + wave * C::WWave;
+        const int half = lane >> 5;
+        uint4 wc[CT][2];
+#pragma unroll
+        for (int c = 0; c < CT; ++c)
+#pragma unroll
+            for (int b = 0; b < 2; ++b) wc[c][b] = *reinterpret_cast<const uint4*>(wb + c * 2048 + b * 1024 + 16 * lane);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            // the block's codes of each group as the bf16 operands of its two 16-deep steps, and the fp16 scales of
+            // the lane's accumulator rows 8 q + 4 h .. + 3 as fp32
+            bf16x8 wop[CT][2];
+            float dw[CT][16];
+#pragma unroll
+            for (int c = 0; c < CT; ++c) {
+                wop[c][0] = codes_bf16(wc[c][b].x, wc[c][b].y);
+                wop[c][1] = codes_bf16(wc[c][b].z, wc[c][b].w);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint4 r4 = *reinterpret_cast<const uint4*>(wb + CT * 2048 + c * 128 + 32 * q + 16 * half);
+                    const uint32_t w4[4] = {r4.x, r4.y, r4.z, r4.w};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) dw[c][4 * q + j] = half_bits_to_float((uint16_t)(w4[j] >> (16 * b)));
+                }
+            }
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                // high and low parts of the row's k-steps 2 b and 2 b + 1 (chunk 2 step + h of the row, swizzled)
+                const int row = 32 * rt + (lane & 31);
+                bf16x8 xh[2], xl[2];
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    const int chunk = (2 * (2 * b + kk) + half) ^ ((row >> 1) & 7);
+                    xh[kk] = *reinterpret_cast<const bf16x8*>(ab + row * 128 + 16 * chunk);
+                    xl[kk] = *reinterpret_cast<const bf16x8*>(ab + C::BM * 128 + row * 128 + 16 * chunk);
+                }
+#pragma unroll
+                for (int c = 0; c < CT; ++c) {
+                    f32x16 s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wop[c][0], xh[0], f32x16{}, 0, 0, 0);
+                    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wop[c][1], xh[1], s, 0, 0, 0);
+                    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wop[c][0], xl[0], s, 0, 0, 0);
+                    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wop[c][1], xl[1], s, 0, 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) acc[rt][c][e] = fmaf(s[e], dw[c][e], acc[rt][c][e]);
+                }
+            }
+        }
+    };
+    // the segment's pipeline in the fold modes (INT8, EXACT)
+    auto run_segment_fold = [&](int m0, int n0, int k0, int S) __attribute__((always_inline)) {
         start_tile(m0, n0, k0);
         __syncthreads();  // every wave is done with the previous segment's LDS
         issue_a(0);
@@ -585,14 +668,17 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
                 issue_a(s + 2);
                 issue_w(s + 2);
             }
-            compute_i8(s % 3);
+            if constexpr (I8)
+                compute_i8(s % 3);
+            else
+                compute_ex(s % 3);
         }
     };
 
     // ---- one segment: stages k0 .. k0 + S - 1 of the tile at (m0, n0), accumulated from zero into acc
     auto run_segment = [&](int m0, int n0, int k0, int S) __attribute__((always_inline)) {
-        if constexpr (I8) {
-            run_segment_i8(m0, n0, k0, S);
+        if constexpr (I8 || EX) {
+            run_segment_fold(m0, n0, k0, S);
             return;
         }
         start_tile(m0, n0, k0);
@@ -732,7 +818,7 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
                     // in kH passes of kP uint4 pieces (register budget); in a pass every stored part is read with
                     // one batch of loads (one round trip per part): the parts before this one are summed into t,
                     // then this part's own pieces are added to t, then the parts after it.
-                    constexpr int kH = RT >= 8 || I8 ? 4 : 2, kP = kQ / kH;  // I8: within 256 VGPRs
+                    constexpr int kH = RT >= 8 || FOLD ? 4 : 2, kP = kQ / kH;  // fold modes: within 256 VGPRs
                     auto slot_off = [&](int c) __attribute__((always_inline)) {
                         return (2 * c + (t0 > begin_of(c) ? 1 : 0)) * kSlot + tid * 16;
                     };
@@ -790,10 +876,10 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
     }
 }
 
-template <typename T, int RT, int CT, int ACT, bool FAST, bool RES, bool SPLIT, bool Q4K = false, bool I8 = false>
+template <typename T, int RT, int CT, int ACT, bool FAST, bool RES, bool SPLIT, bool Q4K = false, int FOLD = 0>
 __global__ __launch_bounds__(kWideThreads) void q8_wide_kernel(GemmParams p, WideSplit sp) {
-    __shared__ __attribute__((aligned(1024))) char smem[WideCfg<RT, CT, Q4K, I8>::Lds];
-    wide_tiles<T, RT, CT, ACT, FAST, RES, SPLIT, Q4K, I8>(p, sp, smem);
+    __shared__ __attribute__((aligned(1024))) char smem[WideCfg<RT, CT, Q4K, FOLD>::Lds];
+    wide_tiles<T, RT, CT, ACT, FAST, RES, SPLIT, Q4K, FOLD>(p, sp, smem);
 }
 
 // f(activation, residual present) as compile-time constants, for the register epilogue's activations (the others
@@ -820,7 +906,7 @@ bool below_2gb(const GemmParams& p) {
     return y_end < INT32_MAX && (!p.res || r_end < INT32_MAX);
 }
 
-template <typename T, int RT, int CT, bool SPLIT, bool Q4K, bool I8 = false>
+template <typename T, int RT, int CT, bool SPLIT, bool Q4K, int FOLD = 0>
 int launch_wide_s(GemmParams p, const WideSplit& sp, hipStream_t stream) {
     const dim3 grid(sp.G), block(kWideThreads);
     p.tiles_m = (p.m + 32 * RT - 1) / (32 * RT);
@@ -830,11 +916,11 @@ int launch_wide_s(GemmParams p, const WideSplit& sp, hipStream_t stream) {
                       (!p.bias || p.bias_dt == IDOLQ_F32) &&
                       (p.act == IDOLQ_ACT_NONE || p.act == IDOLQ_ACT_GELU_TANH || p.act == IDOLQ_ACT_RELU);
     if (!fast)
-        hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, IDOLQ_ACT_NONE, false, false, SPLIT, Q4K, I8>), grid, block, 0, stream,
+        hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, IDOLQ_ACT_NONE, false, false, SPLIT, Q4K, FOLD>), grid, block, 0, stream,
                            p, sp);
     else
         with_fast_epilogue(p, [&](auto act, auto res) {
-            hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, decltype(act)::value, true, decltype(res)::value, SPLIT, Q4K, I8>),
+            hipLaunchKernelGGL((q8_wide_kernel<T, RT, CT, decltype(act)::value, true, decltype(res)::value, SPLIT, Q4K, FOLD>),
                                grid, block, 0, stream, p, sp);
         });
     return check_launch("q8_wide_kernel");

@@ -165,8 +165,9 @@ def gemm(x, w, n_total, n_offset=0, n=None, bias=None, residual=None, act=ACT_NO
     layout of tile_q8_0. x is [m, k] (unit-stride rows).
 
     In DEQUANT mode split=True passes the device's cached workspace, which lets the library split the tiles' k range
-    over the CUs (partial tiles); by default whole tiles per workgroup. INT8 mode needs a workspace (allocated here
-    when none is given); on tiled weights split=True lets it use the rest of that workspace the same way."""
+    over the CUs (partial tiles); by default whole tiles per workgroup. INT8 mode, and EXACT mode on tiled weights,
+    need a workspace (allocated here when none is given); on tiled weights split=True lets them use the rest of that
+    workspace the same way."""
     lib = load()
     m, k = x.shape
     if n is None:
@@ -185,8 +186,11 @@ def gemm(x, w, n_total, n_offset=0, n=None, bias=None, residual=None, act=ACT_NO
         raise ValueError("bias must be a contiguous vector of n_total values")
     eff_mode = mode if mode != MODE_AUTO else (MODE_EXACT if x.dtype == torch.float32 else MODE_DEQUANT)
     ws_bytes = int(lib.idolq_q8_0_gemm_workspace(m, k, eff_mode))
-    if eff_mode == MODE_INT8 and not (tiled and split):
-        # the codes and scales alone (the rest of the INT8 workspace is the tiled path's split room)
+    if eff_mode == MODE_EXACT and not tiled:
+        ws_bytes = 0   # the row-major EXACT kernel takes none
+    elif eff_mode in (MODE_INT8, MODE_EXACT) and not (tiled and split):
+        # the INT8 codes and scales or the EXACT high and low parts alone (the rest of the workspace is the tiled
+        # path's split room)
         ws_bytes -= int(lib.idolq_q8_0_gemm_workspace(m, k, MODE_DEQUANT))
     if ws_bytes and (workspace is None or workspace.numel() * workspace.element_size() < ws_bytes):
         if eff_mode == MODE_DEQUANT:

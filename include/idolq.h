@@ -82,7 +82,9 @@ int64_t idolq_q8_0_bytes(int64_t n, int64_t k);
  *   workspace / workspace_bytes  scratch of idolq_q8_0_gemm_workspace bytes: required by IDOLQ_MODE_INT8 (quantized
  *            activations and scales, m * k * 9 / 8 bytes and some padding at the start; with tiled weights the
  *            rest, when present, is used like the DEQUANT workspace and needs no zero-fill: the call clears its
- *            counters); optional for IDOLQ_MODE_DEQUANT with tiled weights, where it lets the k stages of the
+ *            counters); required by IDOLQ_MODE_EXACT with tiled weights (the activations split into bf16 high and
+ *            low parts, m * k * 4 bytes at the start, the rest used the same way); optional for
+ *            IDOLQ_MODE_DEQUANT with tiled weights, where it lets the k stages of the
  *            tiles left after whole rounds of the CUs be split over the CUs (tile counters, then partial tiles). A
  *            DEQUANT workspace must be zero-filled before its first use and used by one stream at a time; calls
  *            leave its counters at zero, ready for the next call.
@@ -95,14 +97,16 @@ int idolq_q8_0_gemm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ld
 
 /* Workspace bytes idolq_q8_0_gemm uses for m rows of depth k in the given mode: the quantized activations and
  * scales, then room for the tiled path's split, for IDOLQ_MODE_INT8; the tile counters and partial tiles of the
- * current device's CUs for IDOLQ_MODE_DEQUANT; 0 for IDOLQ_MODE_EXACT. */
+ * current device's CUs for IDOLQ_MODE_DEQUANT; the high and low parts, then the same split room, for
+ * IDOLQ_MODE_EXACT (used with tiled weights only: the row-major EXACT kernel takes no workspace). */
 size_t idolq_q8_0_gemm_workspace(int64_t m, int64_t k, int mode);
 
 /* idolq_q8_0_gemm for callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc): no workspace argument, and the call allocates nothing. No counterpart in the reference.
- * IDOLQ_MODE_INT8 takes its quantized activations and scales from a static device array of
- * idolq_q8_0_gemm_noalloc_max_bytes() bytes (32 MiB; m * k * 9 / 8 bytes are used, larger m * k is IDOLQ_EINVAL);
- * DEQUANT runs whole tiles (no stream-K split) and EXACT needs no scratch. Each device has its own array, shared by
+ * IDOLQ_MODE_INT8 takes its quantized activations and scales, IDOLQ_MODE_EXACT on tiled weights its bf16 high and
+ * low parts, from a static device array of idolq_q8_0_gemm_noalloc_max_bytes() bytes (32 MiB; INT8 uses
+ * m * k * 9 / 8 bytes, EXACT m * k * 4, a larger need is IDOLQ_EINVAL); every call runs whole tiles (no stream-K
+ * split) and row-major EXACT needs no scratch. Each device has its own array, shared by
  * every call on that device: calls that overlap on one device (several streams or threads at once) race on it. */
 int idolq_q8_0_gemm_noalloc(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* w,
                             int64_t n_total, int64_t n_offset, int64_t n, const void* bias, int bias_dtype,

@@ -5,6 +5,8 @@ Q8_0 expansion) is bit-exact; float outputs are within 1e-3 norm-relative error 
 kernels (EXACT / INT8 modes) and 2e-2 for the bf16-dequant path (DEQUANT), measured against the CPU result rounded
 to the output dtype.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -171,6 +173,75 @@ def test_int8_on_tiled_weights_matches_the_row_major_int8_kernel(m, n_total, k, 
         wrows = wq.reshape(n_total, -1)[off:off + cnt].reshape(-1)
         ref = O.gemm_q8_int8(x.float().cpu().numpy(), wrows, cnt, k, b[off:off + cnt])
         assert norm_rel(til.cpu().numpy(), ref) < 1e-5
+
+
+@pytest.mark.parametrize("m,n_total,k,off,cnt,xdt", [
+    (256, 1024, 1024, 0, 1024, torch.float32),   # config 0's shape, fp32 activations (the reference's input)
+    (300, 520, 512, 32, 448, torch.float32),     # ragged rows and a column window
+    (1, 96, 128, 0, 96, torch.float16),          # one row, two stages
+    (70, 200, 320, 64, 136, torch.bfloat16),     # ragged everything, five stages
+    (512, 512, 4096, 0, 512, torch.float32),     # stream-K (every tile split)
+    (2048, 1536, 1536, 0, 1536, torch.float32),  # a full wave of tiles and a partial one
+])
+def test_exact_on_tiled_weights_matches_the_row_major_exact_kernel(m, n_total, k, off, cnt, xdt):
+    # EXACT mode on tiled weights (activations split into bf16 high and low parts, two bf16 MFMA products per block,
+    # the block scale folded in fp32) against the row-major EXACT kernel and the oracle's float kernel: both within
+    # 1e-5 of the oracle, within 1e-6 of each other (fp32 reassociation only); with the k range split over the CUs
+    # repeated calls are bit-identical and every tile counter ends at zero (an explicit workspace whose counters
+    # start as garbage: the split prepass clears them)
+    print(f"exact tiled m={m} n={n_total} k={k} window {off}+{cnt} {xdt}", flush=True)
+    rng = np.random.default_rng(m + k + 1)
+    a = rng.normal(0, 1, (m, k)).astype(np.float32)
+    wq = q8(rng, n_total, k)
+    b = rng.normal(0, 0.01, n_total).astype(np.float32)
+    x, wd, bt = to_dev(a).to(xdt), to_dev(wq), to_dev(b)
+    wt = L.tile_q8_0(wd, n_total, k)
+    kw = dict(bias=bt, mode=L.MODE_EXACT, out_dtype=torch.float32)
+    raw = L.gemm(x, wd, n_total, off, cnt, **kw)
+    til = L.gemm(x, wt, n_total, off, cnt, tiled=True, **kw)
+    lib = L.load()
+    full = int(lib.idolq_q8_0_gemm_workspace(m, k, L.MODE_EXACT))
+    prefix = full - int(lib.idolq_q8_0_gemm_workspace(m, k, L.MODE_DEQUANT))
+    assert prefix >= 4 * m * k
+    ws = torch.zeros(full, device=DEV, dtype=torch.uint8)
+    ws[prefix:prefix + 4096] = 7
+    spl = [L.gemm(x, wt, n_total, off, cnt, tiled=True, split=True, workspace=ws, **kw) for _ in range(2)]
+    torch.cuda.synchronize()
+    assert norm_rel(til.cpu().numpy(), raw.cpu().numpy()) < 1e-6
+    assert torch.equal(spl[0], spl[1])
+    assert norm_rel(spl[0].cpu().numpy(), til.cpu().numpy()) < 1e-6
+    assert int(ws[prefix:prefix + 4096].view(torch.int32).abs().sum().item()) == 0
+    if m * k <= 2 ** 20:
+        wrows = wq.reshape(n_total, -1)[off:off + cnt].reshape(-1)
+        ref = O.gemm_q8_float(x.float().cpu().numpy(), wrows, cnt, k, b[off:off + cnt])
+        assert norm_rel(til.cpu().numpy(), ref) < 1e-5
+
+
+def test_exact_on_tiled_weights_epilogue_and_workspace_check():
+    # fp32 output with bias, residual aliasing y and erf-GELU (the reference's float-kernel epilogue) through the
+    # tiled EXACT path, against the row-major EXACT kernel; a workspace below the high and low parts is refused
+    rng = np.random.default_rng(33)
+    m, n, k = 333, 416, 768
+    x = to_dev(rng.normal(0, 1, (m, k)).astype(np.float32))
+    wq = to_dev(q8(rng, n, k))
+    wt = L.tile_q8_0(wq, n, k)
+    bt = to_dev(rng.normal(0, 0.1, n).astype(np.float32))
+    res = to_dev(rng.normal(0, 1, (m, n)).astype(np.float32))
+    outs = []
+    for w, tiled in ((wq, False), (wt, True)):
+        y = res.clone()
+        L.gemm(x, w, n, bias=bt, residual=y, act=L.ACT_GELU_ERF, mode=L.MODE_EXACT, out=y, tiled=tiled)
+        outs.append(y)
+    torch.cuda.synchronize()
+    assert norm_rel(outs[1].cpu().numpy(), outs[0].cpu().numpy()) < 1e-6
+    lib = L.load()
+    small = torch.zeros(4 * m * k - 256, device=DEV, dtype=torch.uint8)
+    y = torch.empty((m, n), device=DEV)
+    rc = lib.idolq_q8_0_gemm(ctypes.c_void_p(x.data_ptr()), L.F32, m, k, k, ctypes.c_void_p(wt.data_ptr()), n, 0, n,
+                             None, 0, None, 0, 0, L.ACT_NONE, L.MODE_EXACT, L.FLAG_TILED_WEIGHTS,
+                             ctypes.c_void_p(y.data_ptr()), L.F32, n, ctypes.c_void_p(small.data_ptr()), small.numel(),
+                             ctypes.c_void_p(torch.cuda.current_stream(DEV).cuda_stream))
+    assert rc == L.EINVAL and b"workspace" in lib.idolq_last_error()
 
 
 def test_int8_on_tiled_weights_register_epilogue():

@@ -46,7 +46,9 @@ def test_c_abi_rejects_bad_arguments_on_the_host():
     lib = L.load()
     assert lib.idolq_q8_0_bytes(6144, 1536) == 6144 * 48 * 34
     assert lib.idolq_q8_0_bytes(10, 33) == 0
-    assert lib.idolq_q8_0_gemm_workspace(4096, 1536, L.MODE_EXACT) == 0
+    # EXACT: the bf16 high and low parts of the tiled path, then the same split room as DEQUANT
+    assert lib.idolq_q8_0_gemm_workspace(4096, 1536, L.MODE_EXACT) == (
+        4096 * 1536 * 4 + lib.idolq_q8_0_gemm_workspace(4096, 1536, L.MODE_DEQUANT))
     # DEQUANT: one 256 x 128 fp32 partial tile and a flag per CU (256 where no device is visible), and an error word
     assert lib.idolq_q8_0_gemm_workspace(4096, 1536, L.MODE_DEQUANT) >= 256 * (256 * 128 * 4 + 4)
     assert lib.idolq_q8_0_gemm_workspace(4096, 1536, L.MODE_INT8) >= 4096 * 1536 + 4096 * 48 * 4
@@ -65,6 +67,9 @@ def test_c_abi_rejects_bad_arguments_on_the_host():
     assert rc == L.EINVAL and b"DEQUANT" in lib.idolq_last_error()
     rc = lib.idolq_q8_0_gemm(fake, L.BF16, 4, 64, 64, fake, 8, 0, 8, None, 0, None, 0, 0, 0, L.MODE_INT8, 0, fake,
                              L.BF16, 8, None, 0, None)
+    assert rc == L.EINVAL and b"workspace" in lib.idolq_last_error()
+    rc = lib.idolq_q8_0_gemm(fake, L.F32, 4, 64, 64, fake, 8, 0, 8, None, 0, None, 0, 0, 0, L.MODE_EXACT,
+                             L.FLAG_TILED_WEIGHTS, fake, L.F32, 8, None, 0, None)
     assert rc == L.EINVAL and b"workspace" in lib.idolq_last_error()
     rc = lib.idolq_q8_0_gemm(fake, 7, 4, 64, 64, fake, 8, 0, 8, None, 0, None, 0, 0, 0, 0, 0, fake, L.BF16, 8, None,
                              0, None)

@@ -57,6 +57,22 @@ def test_noalloc_int8_on_tiled_weights_matches_the_workspace_gemm():
         assert torch.equal(got, want), (m, n, k)
 
 
+def test_noalloc_exact_on_tiled_weights_matches_the_workspace_gemm():
+    # EXACT on tiled weights takes its bf16 high and low parts from the array (whole tiles): the same bits as the
+    # workspace call without split, on two calls in a row, the second smaller
+    rng = np.random.default_rng(48)
+    for m, n, k in ((1024, 768, 2048), (300, 224, 512)):
+        x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(DEV)
+        w = torch.from_numpy(O.q8_0_quantize(rng.normal(0, 0.02, (n, k)).astype(np.float32))).to(DEV)
+        wt = L.tile_q8_0(w, n, k)
+        b = torch.from_numpy(rng.normal(0, 0.01, n).astype(np.float32)).to(DEV)
+        want = L.gemm(x, wt, n, bias=b, act=L.ACT_GELU_ERF, mode=L.MODE_EXACT, out_dtype=torch.float32, tiled=True)
+        got = torch.full((m, n), float("nan"), device=DEV)
+        assert _call_noalloc(x, wt, n, n, b, L.MODE_EXACT, got, L.FLAG_TILED_WEIGHTS) == 0, L.load().idolq_last_error()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), (m, n, k)
+
+
 def test_noalloc_gemm_rejects_inputs_beyond_its_scratch():
     lib = L.load()
     cap = int(lib.idolq_q8_0_gemm_noalloc_max_bytes())
@@ -69,3 +85,10 @@ def test_noalloc_gemm_rejects_inputs_beyond_its_scratch():
     out = torch.empty((m, 32), device=DEV)
     assert _call_noalloc(x, w, 32, 32, b, L.MODE_INT8, out) == L.EINVAL
     assert b"scratch" in lib.idolq_last_error()
+    # EXACT on tiled weights needs m * k * 4 bytes
+    m = cap // (4 * k) + 32
+    x = torch.zeros((m, k), device=DEV)
+    wt = torch.zeros(int(lib.idolq_q8_0_tiled_bytes(32, k)), device=DEV, dtype=torch.uint8)
+    out = torch.empty((m, 32), device=DEV)
+    assert _call_noalloc(x, wt, 32, 32, b, L.MODE_EXACT, out, L.FLAG_TILED_WEIGHTS) == L.EINVAL
+    assert b"EXACT" in lib.idolq_last_error()
