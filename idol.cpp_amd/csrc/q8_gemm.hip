@@ -359,17 +359,21 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, const f32x16 (&a
 // Epilogue through LDS: the accumulator tile is written to LDS as fp32 ([BM][BN + 4]), then each thread takes runs of
 // 8 consecutive columns of one row and applies the epilogue with vector loads of bias and residual and one 16-byte
 // (32-byte for fp32) store per run, so each wave writes whole row segments instead of 2-byte scattered stores.
-template <int BM, int BN, int TM, int TN, int WM, int WN, int THREADS>
+// KS == 2: the workgroup's waves form two depth groups and only the first group's accumulators (which already hold
+// the second group's sums) are written.
+template <int BM, int BN, int TM, int TN, int WM, int WN, int THREADS, int KS = 1>
 __device__ __forceinline__ void write_tile_staged(const GemmParams& p, const f32x16 (&acc)[TM][TN], int m0, int n0,
                                                   float* stage) {
     constexpr int kPitch = BN + 4;
     constexpr int kRuns = BN / 8;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wq = wave % (THREADS / 64 / KS);
+    const int wm = wq >> 1, wn = wq & 1;
     const bool round_first = (p.flags & IDOLQ_FLAG_ROUND_BEFORE_BIAS) != 0;
     __syncthreads();
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn) {
+        if (KS == 2 && wave >= THREADS / 128) break;
         const int col = wn * WN + tn * 32 + (lane & 31);
         const float bias = p.bias && n0 + col < p.n ? load_as_float(p.bias, p.bias_dt, n0 + col) : 0.0f;
 #pragma unroll
@@ -441,13 +445,18 @@ __device__ __forceinline__ void write_tile_staged(const GemmParams& p, const f32
 // During stage s each wave stores those registers (A[(s+1)%2], raw[s%2]), reloads them with activations s+3 and
 // weights s+4, converts raw[(s+1)%2] into B[(s+1)%2] and runs the MFMAs of stage s; every buffer it writes was last
 // read in stage s-1, before the barrier that ends it.
-template <int BM, int BN, int XT, int MODE, bool W4, int THREADS>
+// KS == 2 (EXACT): the waves form two depth groups of (THREADS / 256) x 2; group g multiplies block g of every
+// two-block stage into its own accumulators, and the second group's sums are added to the first's at the end (twice
+// the waves per workgroup for the latency of the per-block MFMA chains, the same loads and conversion).
+template <int BM, int BN, int XT, int MODE, bool W4, int THREADS, int KS = 1>
 __global__ __launch_bounds__(THREADS) void q8_gemm_kernel(GemmParams p) {
     typedef typename std::conditional<XT == XT_F16, _Float16, __bf16>::type T;
     typedef typename Mfma<T>::vec Vec;
     constexpr int NT = XT == XT_F32 ? 2 : 1;  // activation terms: bf16 high and low parts of fp32 input
-    // waves in a (THREADS / 128) x 2 grid, each owning a WM x WN tile of 32 x 32 MFMA tiles
-    constexpr int WAVES_M = THREADS / 128;
+    static_assert(KS == 1 || (KS == 2 && MODE == MODE_EXACT), "depth groups are for the EXACT fold");
+    // waves in a (THREADS / KS / 128) x 2 grid per depth group, each owning a WM x WN tile of 32 x 32 MFMA tiles
+    constexpr int WAVES_M = THREADS / KS / 128;
+    constexpr int NB = 2 / KS;  // blocks of a stage each wave multiplies
     constexpr int WM = BM / WAVES_M, WN = BN / 2, TM = WM / 32, TN = WN / 32;
 
     constexpr int kABytes = 2 * NT * BM * kAPitch * 2, kBBytes = 2 * BN * kAPitch * 2, kRawBytes = 2 * BN * 17 * 4;
@@ -465,7 +474,9 @@ __global__ __launch_bounds__(THREADS) void q8_gemm_kernel(GemmParams p) {
     ScaleTile* bscale = reinterpret_cast<ScaleTile*>(smem + kABytes + kBBytes + kRawBytes);
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int kg = KS == 2 ? wave / (THREADS / 128) : 0;  // depth group
+    const int wq = wave % (THREADS / 64 / KS);
+    const int wm = wq >> 1, wn = wq & 1;
     int tile_m, tile_n;
     tile_coords(p.tiles_m, p.tiles_n, tile_m, tile_n);
     const int m0 = tile_m * BM, n0 = tile_n * BN;
@@ -521,32 +532,33 @@ __global__ __launch_bounds__(THREADS) void q8_gemm_kernel(GemmParams p) {
         convert_stage<T, BN, MODE, THREADS>(raw_lds[nxt], b_lds[nxt], bscale[nxt]);
 
         const uint16_t* bc = b_lds[cur];
-        // Operands of both blocks of the stage are read before the first MFMA (the second block's reads complete
-        // under the first block's MFMAs).
-        Vec a[2][NT][TM][2], b[2][TN][2];
+        // Operands of the wave's blocks of the stage are read before the first MFMA (the second block's reads
+        // complete under the first block's MFMAs).
+        Vec a[NB][NT][TM][2], b[NB][TN][2];
 #pragma unroll
-        for (int blk = 0; blk < 2; ++blk)
+        for (int bi = 0; bi < NB; ++bi)
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const int koff = blk * 32 + h * 16 + (lane >> 5) * 8;
+                const int koff = (KS == 2 ? kg : bi) * 32 + h * 16 + (lane >> 5) * 8;
 #pragma unroll
                 for (int t = 0; t < NT; ++t)
 #pragma unroll
                     for (int tm = 0; tm < TM; ++tm)
-                        a[blk][t][tm][h] = *reinterpret_cast<const Vec*>(a_lds[cur][t] + (wm * WM + tm * 32 + (lane & 31)) * kAPitch + koff);
+                        a[bi][t][tm][h] = *reinterpret_cast<const Vec*>(a_lds[cur][t] + (wm * WM + tm * 32 + (lane & 31)) * kAPitch + koff);
 #pragma unroll
                 for (int tn = 0; tn < TN; ++tn)
-                    b[blk][tn][h] = *reinterpret_cast<const Vec*>(bc + (wn * WN + tn * 32 + (lane & 31)) * kAPitch + koff);
+                    b[bi][tn][h] = *reinterpret_cast<const Vec*>(bc + (wn * WN + tn * 32 + (lane & 31)) * kAPitch + koff);
             }
 #pragma unroll
-        for (int blk = 0; blk < 2; ++blk) {
+        for (int bi = 0; bi < NB; ++bi) {
+            const int blk = KS == 2 ? kg : bi;
 #pragma unroll
             for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
                 for (int tn = 0; tn < TN; ++tn) {
                     if (MODE == MODE_DEQUANT) {
-                        acc[tm][tn] = Mfma<T>::run(a[blk][0][tm][0], b[blk][tn][0], acc[tm][tn]);
-                        acc[tm][tn] = Mfma<T>::run(a[blk][0][tm][1], b[blk][tn][1], acc[tm][tn]);
+                        acc[tm][tn] = Mfma<T>::run(a[bi][0][tm][0], b[bi][tn][0], acc[tm][tn]);
+                        acc[tm][tn] = Mfma<T>::run(a[bi][0][tm][1], b[bi][tn][1], acc[tm][tn]);
                     } else {
                         const float d = bscale[cur][(wn * WN + tn * 32 + (lane & 31)) * 2 + blk];
                         f32x16 part;
@@ -554,8 +566,8 @@ __global__ __launch_bounds__(THREADS) void q8_gemm_kernel(GemmParams p) {
                         for (int r = 0; r < 16; ++r) part[r] = 0.0f;
 #pragma unroll
                         for (int t = 0; t < NT; ++t) {
-                            part = Mfma<T>::run(a[blk][t][tm][0], b[blk][tn][0], part);
-                            part = Mfma<T>::run(a[blk][t][tm][1], b[blk][tn][1], part);
+                            part = Mfma<T>::run(a[bi][t][tm][0], b[bi][tn][0], part);
+                            part = Mfma<T>::run(a[bi][t][tm][1], b[bi][tn][1], part);
                         }
 #pragma unroll
                         for (int r = 0; r < 16; ++r) acc[tm][tn][r] = fmaf(part[r], d, acc[tm][tn][r]);
@@ -569,7 +581,32 @@ __global__ __launch_bounds__(THREADS) void q8_gemm_kernel(GemmParams p) {
         stage(s, as1, ws0);
         if (s + 1 < nsteps) stage(s + 1, as0, ws1);
     }
-    write_tile_staged<BM, BN, TM, TN, WM, WN, THREADS>(p, acc, m0, n0, reinterpret_cast<float*>(smem));
+    if constexpr (KS == 2) {
+        // the second group's sums (odd blocks) through LDS into the first group's (even blocks): a fixed order
+        float* red = reinterpret_cast<float*>(smem);
+        constexpr int kPitch = BN + 4;
+        __syncthreads();
+        if (kg == 1)
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        red[(wm * WM + tm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * kPitch + wn * WN + tn * 32 +
+                            (lane & 31)] = acc[tm][tn][r];
+        __syncthreads();
+        if (kg == 0)
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        acc[tm][tn][r] += red[(wm * WM + tm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * kPitch +
+                                              wn * WN + tn * 32 + (lane & 31)];
+    }
+    write_tile_staged<BM, BN, TM, TN, WM, WN, THREADS, KS>(p, acc, m0, n0, reinterpret_cast<float*>(smem));
 }
 
 // ------------------------------------------------------------------------------------------------ int8 MFMA kernel
@@ -704,15 +741,16 @@ int launch_16bit_tile(GemmParams p, int xt, int mode, bool w4, hipStream_t strea
     return check_launch("q8_gemm_kernel");
 }
 
+// fp32 activations (EXACT): eight waves in two depth groups (the even and the odd block of each stage)
 template <int BM, int BN>
 int launch_f32_tile(GemmParams p, bool w4, hipStream_t stream) {
     p.tiles_m = (p.m + BM - 1) / BM;
     p.tiles_n = (p.n + BN - 1) / BN;
-    const dim3 grid(p.tiles_m * p.tiles_n), block(kThreads);
+    const dim3 grid(p.tiles_m * p.tiles_n), block(2 * kThreads);
     if (w4)
-        hipLaunchKernelGGL((q8_gemm_kernel<BM, BN, XT_F32, MODE_EXACT, true, kThreads>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((q8_gemm_kernel<BM, BN, XT_F32, MODE_EXACT, true, 2 * kThreads, 2>), grid, block, 0, stream, p);
     else
-        hipLaunchKernelGGL((q8_gemm_kernel<BM, BN, XT_F32, MODE_EXACT, false, kThreads>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((q8_gemm_kernel<BM, BN, XT_F32, MODE_EXACT, false, 2 * kThreads, 2>), grid, block, 0, stream, p);
     return check_launch("q8_gemm_kernel");
 }
 
