@@ -34,6 +34,10 @@ struct AttnParams {
     int64_t lq, lk, heads, head_dim;
     int64_t ldq, ldkv, q_bs, kv_bs, ldo, o_bs;
     float scale_log2;  // log2(e) / sqrt(head_dim)
+    // V staged ahead of attn_mfma_hd64<bf16, true> by attn_v_tiles: fp16 V^T tiles and their exponents
+    const uint16_t* vt;
+    const int* vexps;
+    int64_t ntiles;
 };
 
 constexpr int kHD = 64;
@@ -63,9 +67,12 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 
-template <typename T>
+// VT (bf16 inputs): V comes as the fp16 V^T tiles attn_v_tiles wrote (scaled by 2^-vexps[tile]), so staging a tile
+// is a copy instead of each workgroup converting, transposing and range-checking it again.
+template <typename T, bool VT = false>
 __global__ __launch_bounds__(256, 3) void attn_mfma_hd64(AttnParams p) {
     typedef typename AttnMfma<T>::vec Vec;
+    static_assert(!VT || std::is_same<T, __bf16>::value, "staged V^T tiles are for bf16 inputs");
     // two key/value tiles in LDS: tile j is read from buffer j % 2 while tile j + 1 is loaded into registers and then
     // written to the other buffer; one barrier per tile publishes the next tile
     __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][kBKV * kKPitch];
@@ -121,13 +128,19 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_hd64(AttnParams p) {
     // per d and dword store
     const int kp = threadIdx.x >> 3, part = threadIdx.x & 7;
     uint4 kr[2], vr[2];
+    int vexp_cur = VT ? p.vexps[(b * p.heads + h) * p.ntiles] : 0;  // VT: the exponent of the next step's tile
+    // VT: thread t copies 32 bytes of the staged tile, d row t / 4, keys 16 (t % 4) .. + 16
+    const uint16_t* vt_bh = VT ? p.vt + ((b * p.heads + h) * p.ntiles) * (kHD * kBKV) : nullptr;
     auto load_tile = [&](int64_t j0) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int64_t key = j0 + 2 * kp + i;
             const uint32_t off = key < p.lk ? (uint32_t)(key * p.ldkv + 8 * part) * 2u : kOff;
             kr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
-            vr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
+            if constexpr (!VT)
+                vr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
+            else
+                vr[i] = *reinterpret_cast<const uint4*>(vt_bh + (j0 / kBKV) * (kHD * kBKV) + 16 * threadIdx.x + 8 * i);
         }
     };
     // the V values of thread-local element e of key kp2 + i (16-bit bits)
@@ -140,6 +153,16 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_hd64(AttnParams p) {
         bool big = false;
 #pragma unroll
         for (int i = 0; i < 2; ++i) *reinterpret_cast<uint4*>(&k_lds[buf][(2 * kp + i) * kKPitch + 8 * part]) = kr[i];
+        if constexpr (VT) {
+            // rows of kVPitch elements are 8-byte aligned: four 8-byte stores
+            uint16_t* dst = &vt_lds[buf][(threadIdx.x >> 2) * kVPitch + 16 * (threadIdx.x & 3)];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                *reinterpret_cast<uint2*>(dst + 8 * i) = make_uint2(vr[i].x, vr[i].y);
+                *reinterpret_cast<uint2*>(dst + 8 * i + 4) = make_uint2(vr[i].z, vr[i].w);
+            }
+            return;
+        }
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const uint16_t b0 = vbits(0, e), b1 = vbits(1, e);
@@ -314,7 +337,10 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_hd64(AttnParams p) {
     // the barrier that publishes it
     auto step = [&](int buf, int64_t j0, bool has_next, auto mask_tag, auto first_tag) __attribute__((always_inline)) {
         int vexp = 0;
-        if constexpr (kWideV) {
+        if constexpr (VT) {
+            vexp = vexp_cur;
+            if (has_next) vexp_cur = p.vexps[(b * p.heads + h) * p.ntiles + (j0 + kBKV) / kBKV];
+        } else if constexpr (kWideV) {
             if ((vote[buf][0] | vote[buf][1] | vote[buf][2] | vote[buf][3]) != 0) vexp = rescale_tile(buf);  // uniform
         }
         if (has_next) load_tile(j0 + kBKV);
@@ -349,6 +375,62 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_hd64(AttnParams p) {
             const int d = t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
             store_from_float(p.out, p.out_dt, obase + d, o[t][r] * inv);
         }
+}
+
+// bf16 V -> the fp16 V^T tiles of attn_mfma_hd64<bf16, true>, once per call instead of once per query workgroup:
+// tile j of (batch b, head h) is 64 d rows x 64 keys at ((b heads + h) ntiles + j) x 4096 elements (keys past lk are
+// 0), scaled by 2^-vexps[...] with the rule of the in-kernel path: a tile holding a finite |v| >= 65504 (no bf16
+// value lies in [65504, 65536)) or an infinity takes vexp = E - 14, E its largest exponent, so every scaled value is
+// below 2^15; other tiles 0. One workgroup per tile; the transpose goes through LDS so the stores are 16-byte rows.
+__global__ __launch_bounds__(256) void attn_v_tiles(AttnParams p, uint16_t* __restrict__ vt, int* __restrict__ vexps) {
+    __shared__ __attribute__((aligned(16))) uint16_t tr[kHD * (kBKV + 8)];
+    __shared__ uint32_t red[2][4];
+    const int64_t j = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kp = tid >> 3, part = tid & 7;
+    const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + b * p.kv_bs + h * kHD;
+    uint4 vr[2];
+    uint32_t ex = 0, fin = 0;  // the largest exponent field (any value) and the largest finite magnitude's bits
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int64_t key = j * kBKV + 2 * kp + i;
+        vr[i] = key < p.lk ? *reinterpret_cast<const uint4*>(vbase + key * p.ldkv + 8 * part) : make_uint4(0, 0, 0, 0);
+        const uint32_t w4[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t m = (w4[e >> 1] >> (16 * (e & 1))) & 0x7fffu;
+            ex = max(ex, m & 0x7f80u);
+            fin = max(fin, m <= 0x7f80u ? m : 0u);  // NaN is not counted, as fabsf(NaN) >= 65504 is false
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        ex = max(ex, (uint32_t)__shfl_xor((int)ex, off));
+        fin = max(fin, (uint32_t)__shfl_xor((int)fin, off));
+    }
+    if (lane == 0) red[0][wave] = ex, red[1][wave] = fin;
+    __syncthreads();
+    ex = max(max(red[0][0], red[0][1]), max(red[0][2], red[0][3]));
+    fin = max(max(red[1][0], red[1][1]), max(red[1][2], red[1][3]));
+    const int vexp = fin >= 0x4780u ? (int)(ex >> 7) - 127 - 14 : 0;
+    const float down = __builtin_bit_cast(float, (uint32_t)(127 - vexp) << 23);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t w0 = e >> 1 == 0 ? vr[0].x : e >> 1 == 1 ? vr[0].y : e >> 1 == 2 ? vr[0].z : vr[0].w;
+        const uint32_t w1 = e >> 1 == 0 ? vr[1].x : e >> 1 == 1 ? vr[1].y : e >> 1 == 2 ? vr[1].z : vr[1].w;
+        const f32x2 f = {bf16_bits_to_float((uint16_t)(w0 >> (16 * (e & 1)))) * down,
+                         bf16_bits_to_float((uint16_t)(w1 >> (16 * (e & 1)))) * down};
+        *reinterpret_cast<f16x2*>(&tr[(8 * part + e) * (kBKV + 8) + 2 * kp]) = __builtin_convertvector(f, f16x2);
+    }
+    __syncthreads();
+    // thread t stores 32 bytes: d row t / 4, keys 16 (t % 4) .. + 16
+    const int d = tid >> 2, c = tid & 3;
+    const uint4 a0 = *reinterpret_cast<const uint4*>(&tr[d * (kBKV + 8) + 16 * c]);
+    const uint4 a1 = *reinterpret_cast<const uint4*>(&tr[d * (kBKV + 8) + 16 * c + 8]);
+    uint16_t* dst = vt + ((b * p.heads + h) * p.ntiles + j) * (kHD * kBKV) + d * kBKV + 16 * c;
+    *reinterpret_cast<uint4*>(dst) = a0;
+    *reinterpret_cast<uint4*>(dst + 8) = a1;
+    if (tid == 0) vexps[(b * p.heads + h) * p.ntiles + j] = vexp;
 }
 
 // ------------------------------------------------------------------------------------------------ fp32 kernel
@@ -558,9 +640,30 @@ __global__ __launch_bounds__(256) void attn_f32_mfma(AttnParams p) {
 
 using namespace idolq;
 
+namespace {
+// The staged V^T tiles and their exponents of a bf16 call with head_dim 64 (0 bytes for any other call).
+size_t attn_workspace_bytes(int dtype, int64_t batch, int64_t lk, int64_t heads, int64_t head_dim) {
+    if (dtype != IDOLQ_BF16 || head_dim != kHD || batch <= 0 || lk <= 0 || heads <= 0) return 0;
+    const size_t tiles = (size_t)batch * (size_t)heads * (size_t)((lk + kBKV - 1) / kBKV);
+    return tiles * kHD * kBKV * 2 + (tiles * 4 + 255) / 256 * 256;
+}
+}  // namespace
+
+extern "C" size_t idolq_attention_workspace(int dtype, int64_t batch, int64_t lk, int64_t heads, int64_t head_dim) {
+    return attn_workspace_bytes(dtype, batch, lk, heads, head_dim);
+}
+
 extern "C" int idolq_attention(const void* q, const void* k, const void* v, int dtype, int64_t batch, int64_t lq,
                                int64_t lk, int64_t heads, int64_t head_dim, int64_t ldq, int64_t ldkv, int64_t q_bs,
                                int64_t kv_bs, void* out, int out_dtype, int64_t ldo, int64_t o_bs, void* stream) {
+    return idolq_attention_ws(q, k, v, dtype, batch, lq, lk, heads, head_dim, ldq, ldkv, q_bs, kv_bs, out, out_dtype,
+                              ldo, o_bs, nullptr, 0, stream);
+}
+
+extern "C" int idolq_attention_ws(const void* q, const void* k, const void* v, int dtype, int64_t batch, int64_t lq,
+                                  int64_t lk, int64_t heads, int64_t head_dim, int64_t ldq, int64_t ldkv, int64_t q_bs,
+                                  int64_t kv_bs, void* out, int out_dtype, int64_t ldo, int64_t o_bs, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
     if (!dtype_ok(dtype) || !dtype_ok(out_dtype)) return fail(IDOLQ_EINVAL, "unknown dtype code");
     if (batch < 0 || lq < 0 || lk <= 0 || heads <= 0 || head_dim <= 0 || head_dim > kMaxHD)
         return fail(IDOLQ_EINVAL, "bad attention shape (needs lk > 0 and 0 < head_dim <= 256)");
@@ -578,6 +681,23 @@ extern "C" int idolq_attention(const void* q, const void* k, const void* v, int 
                          (ldkv * esz) % 16 == 0 && (q_bs * esz) % 16 == 0 && (kv_bs * esz) % 16 == 0;
     if (dtype != IDOLQ_F32 && head_dim == kHD && aligned && lk * ldkv < ((int64_t)1 << 30)) {
         const dim3 grid((unsigned)((lq + kBQ - 1) / kBQ), (unsigned)heads, (unsigned)batch);
+        const size_t need = attn_workspace_bytes(dtype, batch, lk, heads, head_dim);
+        if (need && workspace && workspace_bytes >= need && reinterpret_cast<uintptr_t>(workspace) % 256 == 0 &&
+            (lk + kBKV - 1) / kBKV <= 0x7fffffff) {
+            // bf16: V staged once as fp16 V^T tiles, then the attention copies them
+            p.ntiles = (lk + kBKV - 1) / kBKV;
+            uint16_t* vt = static_cast<uint16_t*>(workspace);
+            int* vexps = reinterpret_cast<int*>(static_cast<char*>(workspace) +
+                                                (size_t)batch * heads * p.ntiles * kHD * kBKV * 2);
+            hipLaunchKernelGGL(attn_v_tiles, dim3((unsigned)p.ntiles, (unsigned)heads, (unsigned)batch), dim3(256), 0, s,
+                               p, vt, vexps);
+            int rc = check_launch("attn_v_tiles");
+            if (rc) return rc;
+            p.vt = vt;
+            p.vexps = vexps;
+            hipLaunchKernelGGL((attn_mfma_hd64<__bf16, true>), grid, dim3(256), 0, s, p);
+            return check_launch("attn_mfma_hd64");
+        }
         if (dtype == IDOLQ_BF16)
             hipLaunchKernelGGL(attn_mfma_hd64<__bf16>, grid, dim3(256), 0, s, p);
         else

@@ -44,6 +44,9 @@ _SIGNATURES = {
                                _vp]),
     "idolq_attention": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _int,
                                _i64, _i64, _vp]),
+    "idolq_attention_ws": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp,
+                                  _int, _i64, _i64, _vp, _sz, _vp]),
+    "idolq_attention_workspace": (_sz, [_int, _i64, _i64, _i64, _i64]),
     "idolq_activation": (_int, [_vp, _int, _i64, _int, _vp]),
     "idolq_pos_embed": (_int, [_vp, _i64, _vp, _i64, _vp, _int, _i64, _vp]),
     "idolq_point_mlp": (_int, [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp,
@@ -330,14 +333,32 @@ def layernorm(x, eps, gamma=None, beta=None, shift=None, scale=None, rows_per_ba
     return out
 
 
-def attention(q, k, v, batch, lq, lk, heads, head_dim, ldq, ldkv, q_bs, kv_bs, out, ldo, o_bs):
-    """Multi-head attention over flat buffers; q/k/v/out may be views into wider projection buffers."""
+def _attention_workspace(device, nbytes):
+    """The attention workspace of the current stream of a device (grown as needed, kept for the process): each call
+    writes its V^T tiles before the attention reads them, and calls on one stream run one after another."""
+    key = (device, torch.cuda.current_stream(device).cuda_stream)
+    ws = _attention_workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(nbytes, device=device, dtype=torch.uint8)
+        _attention_workspaces[key] = ws
+    return ws
+
+
+_attention_workspaces = {}
+
+
+def attention(q, k, v, batch, lq, lk, heads, head_dim, ldq, ldkv, q_bs, kv_bs, out, ldo, o_bs, staged_v=True):
+    """Multi-head attention over flat buffers; q/k/v/out may be views into wider projection buffers. bf16 inputs
+    with head_dim 64 stage V once per call as fp16 V^T tiles in the stream's cached workspace (the same output bits
+    as staged_v=False, which converts V in every query workgroup)."""
     lib = load()
     dev = _require_cuda(q, k, v, out)
     if not (q.dtype == k.dtype == v.dtype):
         raise ValueError("q, k and v must share a dtype")
-    _check(lib.idolq_attention(_ptr(q), _ptr(k), _ptr(v), _code(q), batch, lq, lk, heads, head_dim, ldq, ldkv, q_bs,
-                               kv_bs, _ptr(out), _code(out), ldo, o_bs, _stream(dev)))
+    need = int(lib.idolq_attention_workspace(_code(q), batch, lk, heads, head_dim)) if staged_v else 0
+    ws = _attention_workspace(q.device, need) if need else None
+    _check(lib.idolq_attention_ws(_ptr(q), _ptr(k), _ptr(v), _code(q), batch, lq, lk, heads, head_dim, ldq, ldkv,
+                                  q_bs, kv_bs, _ptr(out), _code(out), ldo, o_bs, _ptr(ws), need, _stream(dev)))
     return out
 
 

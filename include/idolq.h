@@ -167,6 +167,20 @@ int idolq_attention(const void* q, const void* k, const void* v, int dtype, int6
                     int64_t heads, int64_t head_dim, int64_t ldq, int64_t ldkv, int64_t q_bs, int64_t kv_bs, void* out,
                     int out_dtype, int64_t ldo, int64_t o_bs, void* stream);
 
+/* idolq_attention with a workspace of idolq_attention_workspace() bytes (256-byte aligned; the call writes it
+ * before reading it, so it needs no zero-fill): bf16 inputs with head_dim 64 then convert V once per call into
+ * fp16 V^T tiles (scaled per tile where |v| exceeds fp16, by the same rule as without the workspace) instead of
+ * once per query workgroup; the operands and the arithmetic are those of idolq_attention, so are the output bits.
+ * A null or short workspace runs idolq_attention's path. Calls sharing a workspace must not overlap.
+ * Same reference interface as idolq_attention (src/kernels.hpp:81-84). */
+int idolq_attention_ws(const void* q, const void* k, const void* v, int dtype, int64_t batch, int64_t lq, int64_t lk,
+                       int64_t heads, int64_t head_dim, int64_t ldq, int64_t ldkv, int64_t q_bs, int64_t kv_bs,
+                       void* out, int out_dtype, int64_t ldo, int64_t o_bs, void* workspace, size_t workspace_bytes,
+                       void* stream);
+/* Workspace bytes idolq_attention_ws uses for these shapes: the fp16 V^T tiles (batch x heads x ceil(lk / 64) tiles
+ * of 8 KiB) and their exponents for bf16 inputs with head_dim 64; 0 for every other call. */
+size_t idolq_attention_workspace(int dtype, int64_t batch, int64_t lk, int64_t heads, int64_t head_dim);
+
 /* In-place activation over count values: tanh-GELU (src/decoders.cpp:55-71 gelu_tanh), erf-GELU
  * (src/kernels.cpp:826-850) or ReLU. */
 int idolq_activation(void* x, int dtype, int64_t count, int act, void* stream);

@@ -260,3 +260,34 @@ def test_attention_bf16_values_beyond_fp16_range():
             assert norm_rel(got[:, cols], ref[:, cols]) < 1e-3, h
     assert torch.equal(outs[0][:, hd:], outs[1][:, hd:])
     assert float(outs[1][:, :hd].abs().max()) > 1e5
+
+
+@pytest.mark.parametrize("batch,lq,lk,heads", [(1, 200, 300, 2), (2, 1000, 777, 3), (2, 640, 4096, 4), (1, 64, 64, 1)])
+def test_attention_staged_v_tiles_give_the_same_bits(batch, lq, lk, heads):
+    # bf16 inputs with head_dim 64: V converted once per call into fp16 V^T tiles (attn_v_tiles, the workspace entry
+    # point) against V converted in every query workgroup (no workspace): the same operands and arithmetic, so the
+    # same bits; with tiles beyond fp16's range (scaled per tile by the same rule), an infinity-free huge value, and
+    # ragged key and query counts (the last tile's keys past lk are zero in the staged tiles)
+    print(f"staged V batch={batch} lq={lq} lk={lk} heads={heads}", flush=True)
+    rng = np.random.default_rng(batch * 1000 + lk)
+    hd = 64
+    dim = heads * hd
+    q = rng.normal(0, 2.0, (batch * lq, dim)).astype(np.float32)
+    k = rng.normal(0, 2.0, (batch * lk, dim)).astype(np.float32)
+    v = rng.normal(0, 1, (batch * lk, dim)).astype(np.float32)
+    if lk > 130:
+        v[64:128, :hd] *= 1e5
+        v[130, 7] = 3.0e30
+    qd, kd, vd = (to_dev(a).bfloat16() for a in (q, k, v))
+    outs = []
+    for staged in (True, False):
+        out = torch.empty((batch * lq, dim), device=DEV, dtype=torch.bfloat16)
+        L.attention(qd, kd, vd, batch, lq, lk, heads, hd, dim, dim, lq * dim, lk * dim, out, dim, lq * dim,
+                    staged_v=staged)
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    assert torch.isfinite(outs[0].float()).all()
+    lib = L.load()
+    assert lib.idolq_attention_workspace(L.BF16, batch, lk, heads, hd) >= batch * heads * ((lk + 63) // 64) * 8192
+    assert lib.idolq_attention_workspace(L.F16, batch, lk, heads, hd) == 0
