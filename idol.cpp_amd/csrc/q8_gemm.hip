@@ -103,7 +103,9 @@ struct WeightStage {
 // BM rows x 64 k of x per stage in 16-byte units. The per-thread row offsets (in 16-byte units, ~0u for rows
 // outside m) are computed once; a stage only adds its k offset. Unit u = tid + 256 i covers row u / kUnitsPerRow,
 // column unit tid % kUnitsPerRow (the same for every i).
-template <int BM, int XT, int THREADS>
+// XA: x is known to be 16-byte aligned (no runtime test, so the load sequence has no branch for the compiler's
+// wait counts to merge over).
+template <int BM, int XT, int THREADS, bool XA = false>
 struct ActStage {
     static constexpr int kEsz = XT == XT_F32 ? 4 : 2;
     static constexpr int kUnitsPerRow = kKStep * kEsz / 16;  // 8 (16-bit) or 16 (fp32)
@@ -129,7 +131,7 @@ struct ActStage {
     __device__ __forceinline__ void load(const GemmParams& p, int k0) {
         const int kk = k0 + (threadIdx.x % kUnitsPerRow) * kElems;
         const bool kin = kk < p.k;
-        if (p.x_aligned) {
+        if (XA || p.x_aligned) {
 #pragma unroll
             for (int i = 0; i < kPer; ++i) {
                 ok[i] = off[i] != ~0u && kin;
@@ -197,6 +199,9 @@ struct RawStage {
     static constexpr int kUnitsPerRow = W4 ? 17 : 34;
     static constexpr int kUnits = BN * kUnitsPerRow;
     static constexpr int kPer = (kUnits + THREADS - 1) / THREADS;
+    // dwords of one LDS stage: every thread's kPer units have a slot (units past the rows land in padding, so the
+    // stores need no branch, which would make the compiler wait for every outstanding load before them)
+    static constexpr int kWords = W4 ? kPer * THREADS : (kPer * THREADS + 1) / 2;
     uint32_t off[kPer];  // byte offset of the unit within the window (row * row_bytes + part * size), ~0u if unused
     bool second[kPer];   // the unit belongs to the second block of the stage
     uint32_t v[kPer];
@@ -229,13 +234,11 @@ struct RawStage {
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
             const int u = threadIdx.x + i * THREADS;
-            if (u < kUnits) {
-                const uint32_t vi = ok[i] ? v[i] : 0u;
-                if (W4)
-                    raw[u] = vi;
-                else
-                    reinterpret_cast<uint16_t*>(raw)[u] = (uint16_t)vi;
-            }
+            const uint32_t vi = ok[i] ? v[i] : 0u;
+            if (W4)
+                raw[u] = vi;
+            else
+                reinterpret_cast<uint16_t*>(raw)[u] = (uint16_t)vi;
         }
     }
 };
@@ -448,7 +451,7 @@ __device__ __forceinline__ void write_tile_staged(const GemmParams& p, const f32
 // KS == 2 (EXACT): the waves form two depth groups of (THREADS / 256) x 2; group g multiplies block g of every
 // two-block stage into its own accumulators, and the second group's sums are added to the first's at the end (twice
 // the waves per workgroup for the latency of the per-block MFMA chains, the same loads and conversion).
-template <int BM, int BN, int XT, int MODE, bool W4, int THREADS, int KS = 1>
+template <int BM, int BN, int XT, int MODE, bool W4, int THREADS, int KS = 1, bool XA = false>
 __global__ __launch_bounds__(THREADS) void q8_gemm_kernel(GemmParams p) {
     typedef typename std::conditional<XT == XT_F16, _Float16, __bf16>::type T;
     typedef typename Mfma<T>::vec Vec;
@@ -459,14 +462,15 @@ __global__ __launch_bounds__(THREADS) void q8_gemm_kernel(GemmParams p) {
     constexpr int NB = 2 / KS;  // blocks of a stage each wave multiplies
     constexpr int WM = BM / WAVES_M, WN = BN / 2, TM = WM / 32, TN = WN / 32;
 
-    constexpr int kABytes = 2 * NT * BM * kAPitch * 2, kBBytes = 2 * BN * kAPitch * 2, kRawBytes = 2 * BN * 17 * 4;
+    constexpr int kRawWords = RawStage<BN, W4, THREADS>::kWords;
+    constexpr int kABytes = 2 * NT * BM * kAPitch * 2, kBBytes = 2 * BN * kAPitch * 2, kRawBytes = 2 * kRawWords * 4;
     constexpr int kScaleBytes = MODE == MODE_EXACT ? 2 * BN * 2 * 4 : 16;
     constexpr int kLoopBytes = kABytes + kBBytes + kRawBytes + kScaleBytes;
     constexpr int kStageBytes = BM * (BN + 4) * 4;
     __shared__ __attribute__((aligned(16))) char smem[kLoopBytes > kStageBytes ? kLoopBytes : kStageBytes];
     typedef uint16_t ATile[NT][BM * kAPitch];
     typedef uint16_t BTile[BN * kAPitch];
-    typedef uint32_t RawTile[BN * 17];
+    typedef uint32_t RawTile[kRawWords];
     typedef float ScaleTile[MODE == MODE_EXACT ? BN * 2 : 4];
     ATile* a_lds = reinterpret_cast<ATile*>(smem);
     BTile* b_lds = reinterpret_cast<BTile*>(smem + kABytes);
@@ -494,7 +498,7 @@ __global__ __launch_bounds__(THREADS) void q8_gemm_kernel(GemmParams p) {
     // Two register sets for the activation and weight loads, used alternately, so every load is issued two stages
     // before its registers are stored to LDS: set (s + 1) % 2 of activations holds stage s + 1 at the start of
     // stage s, set s % 2 of weights holds stage s + 2.
-    ActStage<BM, XT, THREADS> as0, as1;
+    ActStage<BM, XT, THREADS, XA> as0, as1;
     RawStage<BN, W4, THREADS> ws0, ws1;
     as0.init(p, m0);
     as1.init(p, m0);
@@ -747,7 +751,9 @@ int launch_f32_tile(GemmParams p, bool w4, hipStream_t stream) {
     p.tiles_m = (p.m + BM - 1) / BM;
     p.tiles_n = (p.n + BN - 1) / BN;
     const dim3 grid(p.tiles_m * p.tiles_n), block(2 * kThreads);
-    if (w4)
+    if (w4 && p.x_aligned)
+        hipLaunchKernelGGL((q8_gemm_kernel<BM, BN, XT_F32, MODE_EXACT, true, 2 * kThreads, 2, true>), grid, block, 0, stream, p);
+    else if (w4)
         hipLaunchKernelGGL((q8_gemm_kernel<BM, BN, XT_F32, MODE_EXACT, true, 2 * kThreads, 2>), grid, block, 0, stream, p);
     else
         hipLaunchKernelGGL((q8_gemm_kernel<BM, BN, XT_F32, MODE_EXACT, false, 2 * kThreads, 2>), grid, block, 0, stream, p);
