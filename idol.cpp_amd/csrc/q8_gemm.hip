@@ -168,7 +168,10 @@ struct ActStage {
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
             const int off_lds = (r0 + i * kRowsPerPass) * kAPitch + cu * kElems;
-            const uint4 vi = ok[i] ? v[i] : make_uint4(0, 0, 0, 0);
+            // a mask, not a select: a select of the loaded value lets the compiler branch around the use, and the
+            // joins make its wait counts fall back to waiting for every outstanding load
+            const uint32_t mk = 0u - (uint32_t)ok[i];
+            const uint4 vi = make_uint4(v[i].x & mk, v[i].y & mk, v[i].z & mk, v[i].w & mk);
             if (XT != XT_F32) {
                 *reinterpret_cast<uint4*>(hi + off_lds) = vi;
             } else {
@@ -234,7 +237,7 @@ struct RawStage {
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
             const int u = threadIdx.x + i * THREADS;
-            const uint32_t vi = ok[i] ? v[i] : 0u;
+            const uint32_t vi = v[i] & (0u - (uint32_t)ok[i]);  // a mask, not a select (as in ActStage::store)
             if (W4)
                 raw[u] = vi;
             else
