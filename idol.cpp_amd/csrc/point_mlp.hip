@@ -41,6 +41,7 @@ constexpr int kXBytes = kPoints * kXStride, kHBytes = kPoints * kHStride;
 constexpr int kLds = kXBytes + kHBytes;
 static_assert(4 * kLds <= 163840, "LDS budget: four workgroups per CU");
 static_assert(kXBytes >= kHBytes, "h2 reuses X's bytes");
+static_assert(kHBytes >= kThreads * 16 && kMaxOut * kMid <= kThreads * 4, "the head's weights fit in H's bytes");
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
@@ -112,8 +113,23 @@ __global__ __launch_bounds__(kThreads, 3) void point_mlp_kernel(const float* __r
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int64_t p0 = (int64_t)blockIdx.x * kPoints;
 
-    // ---- x: the tile's features (rows past m repeat the last row; their outputs are not stored) are requested
-    // first, 16 pieces of 8 values per thread, and rounded to bf16 into LDS after the embedding has been computed
+    // Global loads complete in issue order, and a wait for one load waits for every load issued before it: so the
+    // embedding's inputs are requested first (their wait then leaves the features in flight), and the head's
+    // weights (nout x 64 fp32, one float4 per thread) are fetched now and parked in LDS once layer 2 is done,
+    // instead of the head waiting on global loads output by output.
+    // ---- the embedding's item (point i / 6, coordinate (i / 2) % 3, frequencies 8 (i % 2) .. + 8), i = tid; the
+    // threads past the items load item kPoints * 6 - 1 and do not store
+    constexpr int kItems = kPoints * 6;
+    static_assert(kItems <= kThreads, "one embedding item per thread");
+    const int item = min(tid, kItems - 1);
+    const int erow = item / 6, ec = (item >> 1) - 3 * erow, ej0 = 8 * (item & 1);
+    const float ev = coords[min(p0 + erow, m - 1) * 3 + ec];
+    float ef[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ef[j] = freqs[ej0 + j];
+    const float4 whv = reinterpret_cast<const float4*>(wh)[min(tid, nout * (kMid / 4) - 1)];
+    // ---- x: the tile's features (rows past m repeat the last row; their outputs are not stored), 16 pieces of 8
+    // values per thread, rounded to bf16 into LDS after the embedding has been computed
     constexpr int kPieces = kPoints * (kFeat / 8) / kThreads;
     float4 fv[kPieces][2];
 #pragma unroll
@@ -124,22 +140,21 @@ __global__ __launch_bounds__(kThreads, 3) void point_mlp_kernel(const float* __r
         fv[j][0] = f[0];
         fv[j][1] = f[1];
     }
-    // ---- the embedding: coordinate c of a point fills values 256 + 32 c + j (sine) and + 16 (cosine), j < 16;
-    // item i: point i / 6, coordinate (i / 2) % 3, frequencies 8 (i % 2) .. + 8 (three items per thread)
-    for (int i = tid; i < kPoints * 6; i += kThreads) {
-        const int row = i / 6, c = (i >> 1) - 3 * row, j0 = 8 * (i & 1);
-        const float v = coords[min(p0 + row, m - 1) * 3 + c];
+    // ---- the embedding: coordinate c of a point fills values 256 + 32 c + j (sine) and + 16 (cosine), j < 16
+    {
         const float kPi = 3.14159265358979323846f;
         uint32_t sn[4], cs[4];
 #pragma unroll
         for (int j = 0; j < 8; j += 2) {
-            const float a0 = (v * freqs[j0 + j]) * kPi, a1 = (v * freqs[j0 + j + 1]) * kPi;
+            const float a0 = (ev * ef[j]) * kPi, a1 = (ev * ef[j + 1]) * kPi;
             sn[j / 2] = pack_bf16(sinf(a0), sinf(a1));
             cs[j / 2] = pack_bf16(cosf(a0), cosf(a1));
         }
-        char* dst = X + row * kXStride + 2 * (kFeat + 32 * c + j0);
-        *reinterpret_cast<uint4*>(dst) = make_uint4(sn[0], sn[1], sn[2], sn[3]);
-        *reinterpret_cast<uint4*>(dst + 32) = make_uint4(cs[0], cs[1], cs[2], cs[3]);
+        if (tid < kItems) {
+            char* dst = X + erow * kXStride + 2 * (kFeat + 32 * ec + ej0);
+            *reinterpret_cast<uint4*>(dst) = make_uint4(sn[0], sn[1], sn[2], sn[3]);
+            *reinterpret_cast<uint4*>(dst + 32) = make_uint4(cs[0], cs[1], cs[2], cs[3]);
+        }
     }
 #pragma unroll
     for (int j = 0; j < kPieces; ++j) {
@@ -153,6 +168,10 @@ __global__ __launch_bounds__(kThreads, 3) void point_mlp_kernel(const float* __r
     wide_layer<kK1 / 16>(X, kXStride, w1, b1, H, wave, lane);
     __syncthreads();
     wide_layer<kHidden / 16>(H, kHStride, w2, b2, X, wave, lane);
+    __syncthreads();
+    // h1 is dead: its bytes take the head's weights ([nout][64] fp32, 4 KB at most)
+    float* const whs = reinterpret_cast<float*>(H);
+    reinterpret_cast<float4*>(whs)[tid] = whv;
     __syncthreads();
 
     if (wave >= kTiles) return;  // no barrier follows
@@ -194,7 +213,7 @@ __global__ __launch_bounds__(kThreads, 3) void point_mlp_kernel(const float* __r
 #pragma unroll
     for (int o = 0; o < kMaxOut; ++o) {
         if (o < nout) {
-            const float* wo = wh + o * kMid + 32 * h;
+            const float* wo = whs + o * kMid + 32 * h;
             float part = 0.0f;
 #pragma unroll
             for (int k = 0; k < 32; ++k) part = fmaf(h3[k], wo[k], part);
@@ -223,8 +242,8 @@ extern "C" int idolq_point_mlp(const float* feats, int64_t m, int64_t ldf, const
     if (!feats || !coords || !freqs || !w1 || !b1 || !w2 || !b2 || !w3 || !b3 || !wh || !y)
         return fail(IDOLQ_EINVAL, "null pointer");
     auto al = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
-    if (!al(feats) || !al(w1) || !al(w2) || !al(w3) || !al(b1) || !al(b2))
-        return fail(IDOLQ_EINVAL, "features, weights and the 256-wide biases must be 16-byte aligned");
+    if (!al(feats) || !al(w1) || !al(w2) || !al(w3) || !al(b1) || !al(b2) || !al(wh))
+        return fail(IDOLQ_EINVAL, "features, weights, the head and the 256-wide biases must be 16-byte aligned");
     if (m > (int64_t)INT32_MAX * kPoints / 2) return fail(IDOLQ_EINVAL, "too many points");
     const unsigned blocks = (unsigned)((m + kPoints - 1) / kPoints);
     hipLaunchKernelGGL(point_mlp_kernel, dim3(blocks), dim3(kThreads), 0, static_cast<hipStream_t>(stream), feats, m,
