@@ -1,6 +1,6 @@
 #pragma once
 // The grouped-layout Q8_0 GEMM kernel template shared by q8_gemm_wide.hip (DEQUANT and Q4_K on tiled / row-major
-// weights) and q8_gemm_wide_i8.hip (INT8 mode on tiled weights), with the launch pieces both use. Each source
+// weights) and q8_gemm_wide_fold.hip (INT8 and EXACT modes on tiled weights), with the launch pieces both use. Each source
 // file instantiates its own kernels (internal linkage).
 //
 // Q8_0 GEMM for gfx950 on the grouped weight layout (idolq_q8_0_tile), DEQUANT arithmetic: y = epilogue(x * W^T),
