@@ -3,7 +3,7 @@
  *
  * TEST INFRASTRUCTURE ONLY. Nothing in the product (the HIP library or the Python host modules) may link, load or
  * call this code. It is imported by tests/, by __graft_entry__.smoke() and by bench.py's cpu_baseline leg, and
- * only as the checker, never as the thing measured or shipped.
+ * only to check results against, never as the thing measured or shipped.
  *
  * Every function cites the reference file:line it restates (paths relative to the reference checkout). All
  * functions are single-precision IEEE code built with -ffp-contract=off; where the reference build fuses a

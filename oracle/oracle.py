@@ -1,7 +1,7 @@
 """ctypes bindings for the CPU oracle (liboracle.so) and the reference build (_ref/libidolref.so).
 
-TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg, as the
-checker. The product (idol.cpp_amd/) never imports this module.
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg, to check
+results against. The product (idol.cpp_amd/) never imports this module.
 
 All functions take and return numpy arrays (C-contiguous). Q8_0 weights are uint8 arrays of n * (k / 32) * 34
 bytes; panel blobs are the native layout of the reference's src/kernels.hpp:33-51.

@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the GPU path's checker.
+"""Pins the CPU oracle (oracle/oracle.c) before the GPU path is checked against it.
 
 Three kinds of pin, chosen so that a plausible slip (a dropped term, a wrong sign, index or rounding rule, a
 transposed operand, a changed summation order) fails at least one:
