@@ -727,7 +727,7 @@ def run_cpu_baseline(args, inputs):
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py runs on exactly one GPU: this build has no multi-GPU path (--gpus must be 1)", file=sys.stderr)
+        print("bench.py runs on exactly one GPU: the library has no multi-GPU path (--gpus must be 1)", file=sys.stderr)
         sys.exit(2)
     if args.traffic_probe:
         run_traffic_probe(args)

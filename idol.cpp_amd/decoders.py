@@ -441,7 +441,7 @@ def _rep_vector(dec):
 
 
 def _sample_anchors(self, cond, cond_rows, num_points, level, seed):
-    """Decoders::sample_anchors: the octree descent with this build's octree_logits on the GPU (num_points x 3 fp32,
+    """Decoders::sample_anchors: the octree descent with this module's octree_logits on the GPU (num_points x 3 fp32,
     on the host). The draws follow the reference's generator, so given the same logits the anchors are the
     reference's; logits differing in the last bits can move a point to a sibling cell where a draw falls on a
     cumulative-probability boundary."""

@@ -2,7 +2,7 @@
 tools/idol_packed.py (PackedLinear, enable_fused_packed, replace_quantized_linear_layers).
 
 Signatures, attributes (`shape`, `kind`, `packed` buffer, `bias`, `fused`), the accepted inputs and the error
-messages are the reference's interface; the code is this build's. The fused GPU path is libidolq
+messages are the reference's interface; the code is this package's own. The fused GPU path is libidolq
 (idol_hip.fused_linear) for Q4_0, Q8_0 and Q4_K, the kinds the reference fuses. dequantize() expands every kind: on the GPU with libidolq's kernels (idolq_q8_0_dequant,
 idolq_blocks_dequant), for a module kept on the host with tensor arithmetic; both compute each value with the
 reference expansion's fp32 operations (tools/idol_packed.py:25-71), then round once.

@@ -210,7 +210,7 @@ def test_model_width_export_matches_the_reference_decoders(tmp_path):
 @pytest.mark.parametrize("quant", ["Q8_0", "Q4_0"])
 def test_decoders_from_gguf_match_the_reference(tmp_path, quant):
     # an Idol GGUF (Q8_0 or Q4_0 matrices, F32 / F16 vectors) run three ways: the reference's decoders on the
-    # materialized native export, this build on the same export, and this build straight from the GGUF
+    # materialized native export, these decoders on the same export, and these decoders straight from the GGUF
     import idol_gguf as G
     from ggml_types import GGMLQuantizationType as Q
     from gguf_fixture import write_idol_gguf
@@ -241,7 +241,7 @@ def test_decoders_from_gguf_match_the_reference(tmp_path, quant):
 
 def test_to_gaussians_sample_anchors_and_decode_match_the_reference():
     # src/decoders.cpp:335-442 around the decoders: to_gaussians on the same features (libm-level differences only),
-    # the octree descent with this build's logits, and decode end to end
+    # the octree descent with the GPU decoders' logits, and decode end to end
     _needs_ref()
     from decoders import GaussianCloud, write_gaussian_ply  # noqa: F401
     dec = Decoders(GOLDEN / "decoders_small")
