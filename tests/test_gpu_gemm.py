@@ -97,17 +97,24 @@ def test_int8_mfma_block_dots_are_bit_exact(m, n, k, off, cnt):
 
 def test_gemm_against_reference_golden_vectors(golden):
     # The reference's own outputs for its test shapes (tests/golden/gemm_q8.npz): EXACT vs the float kernel and INT8
-    # vs the integer kernel, fp32 in and out, each within 1e-3 norm-relative (EXACT is ~1e-6 in practice).
+    # vs the integer kernel, fp32 in and out, each within 1e-5 norm-relative, on row-major Q8_0 blocks and (five of
+    # the ten cases) on the tiled layout.
     g = golden("gemm_q8")
     for i in range(int(g["cases"])):
         m, n, k, off, cnt, res, gelu = (int(v) for v in g[f"c{i}_shape"])
         a, w, bias = g[f"c{i}_a"], g[f"c{i}_w"], g[f"c{i}_bias"]
         r = to_dev(g[f"c{i}_residual"]) if res else None
         act = L.ACT_GELU_ERF if gelu else L.ACT_NONE
-        for mode, key, bar in ((L.MODE_EXACT, "y_float", 1e-5), (L.MODE_INT8, "y_int8", 1e-5)):
-            y = L.gemm(to_dev(a), to_dev(w), n, off, cnt, bias=to_dev(bias), residual=r, act=act, mode=mode)
-            err = norm_rel(y.cpu().numpy(), g[f"c{i}_{key}"])
-            assert err < bar, (i, key, err)
+        # the same weights in the tiled layout where it applies (k % 64 == 0, window starting at a multiple of 32)
+        layouts = [(to_dev(w), False)]
+        if k % 64 == 0 and off % 32 == 0:
+            layouts.append((L.tile_q8_0(to_dev(w), n, k), True))
+        for wd, tiled in layouts:
+            for mode, key, bar in ((L.MODE_EXACT, "y_float", 1e-5), (L.MODE_INT8, "y_int8", 1e-5)):
+                y = L.gemm(to_dev(a), wd, n, off, cnt, bias=to_dev(bias), residual=r, act=act, mode=mode,
+                           tiled=tiled)
+                err = norm_rel(y.cpu().numpy(), g[f"c{i}_{key}"])
+                assert err < bar, (i, key, tiled, err)
 
 
 @pytest.mark.parametrize("m,n,k", [(256, 1024, 1024), (70, 100, 352), (33, 37, 64), (5, 21, 32), (300, 96, 1280)])
