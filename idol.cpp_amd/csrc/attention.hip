@@ -38,6 +38,7 @@ struct AttnParams {
     const uint16_t* vt;
     const int* vexps;
     int64_t ntiles;
+    int out_vec;  // out has the input dtype and 16-byte aligned rows and batches: rows go out as 16-byte stores
 };
 
 constexpr int kHD = 64;
@@ -365,8 +366,38 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_hd64(AttnParams p) {
     }
 
     const float l_run = l_part + __shfl_xor(l_part, 32);
-    if (qi >= p.lq) return;
     const float inv = 1.0f / l_run;
+    if (p.out_vec) {
+        // the wave's 32 query rows x 64 d in the input type through its part of k_lds (free after the last tile's
+        // barrier), then read back as whole 16-byte pieces of rows: four row-contiguous stores per lane instead of
+        // 32 scattered 2-byte ones
+        uint16_t* ob = &k_lds[0][0] + wave * 32 * kKPitch;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                const int d = t * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                const float v0 = o[t][r] * inv, v1 = o[t][r + 1] * inv;
+                const uint32_t w = std::is_same<T, __bf16>::value
+                                       ? (uint32_t)float_to_bf16_bits(v0) | ((uint32_t)float_to_bf16_bits(v1) << 16)
+                                       : (uint32_t)float_to_half_bits(v0) | ((uint32_t)float_to_half_bits(v1) << 16);
+                *reinterpret_cast<uint32_t*>(&ob[(lane & 31) * kKPitch + d]) = w;
+            }
+        // the wave's LDS operations run in order; the fences keep the compiler from moving the reads above the writes
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = lane + 64 * i, row = c >> 3, cc = c & 7;
+            const uint4 v = *reinterpret_cast<const uint4*>(&ob[row * kKPitch + 8 * cc]);
+            const int64_t q = q0 + row;
+            if (q < p.lq)
+                *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.out) + b * p.o_bs + q * p.ldo + h * kHD + 8 * cc) = v;
+        }
+        return;
+    }
+    if (qi >= p.lq) return;
     const int64_t obase = b * p.o_bs + qi * p.ldo + h * kHD;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
@@ -674,6 +705,8 @@ extern "C" int idolq_attention_ws(const void* q, const void* k, const void* v, i
     if (!q || !k || !v || !out) return fail(IDOLQ_EINVAL, "q, k, v and out must be non-null");
     AttnParams p{q, k, v, out, dtype, out_dtype, lq, lk, heads, head_dim, ldq, ldkv, q_bs, kv_bs, ldo, o_bs,
                  1.4426950408889634f / sqrtf((float)head_dim)};
+    p.out_vec = out_dtype == dtype && dtype != IDOLQ_F32 && reinterpret_cast<uintptr_t>(out) % 16 == 0 &&
+                (ldo * 2) % 16 == 0 && (o_bs * 2) % 16 == 0;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const size_t esz = dtype_size(dtype);
     const bool aligned = reinterpret_cast<uintptr_t>(q) % 16 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
