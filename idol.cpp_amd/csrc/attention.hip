@@ -10,7 +10,9 @@
 // same fp16 values with dot2); the MFMA's k order is permuted to the order in which the score accumulator holds the
 // keys, and the V^T operand is read in that same order. bf16 values of V beyond fp16's range (|v| >= 65504) are
 // staged scaled by a power of two per tile and the tile's product is scaled back exactly, so the fp16 P * V never
-// overflows where the reference's fp32 attention does not.
+// overflows where the reference's fp32 attention does not. With a workspace (idolq_attention_ws), attn_v_tiles
+// converts bf16 V into those fp16 V^T tiles once per call and the workgroups copy them (the same operands, so the
+// same bits). 16-bit outputs leave through LDS as 16-byte row pieces.
 //
 // attn_f32_mfma (fp32 inputs, head_dim 32 or 64, 16-byte aligned rows): fp32 matrix cores for both products, the key
 // range split over the 4 waves of a 32-query workgroup; the reference's float attention surface at fp32 accuracy.
