@@ -347,14 +347,20 @@ def _attention_workspace(device, nbytes):
 _attention_workspaces = {}
 
 
-def attention(q, k, v, batch, lq, lk, heads, head_dim, ldq, ldkv, q_bs, kv_bs, out, ldo, o_bs, staged_v=True):
+STAGED_V_MIN_KEYS = 2048  # measured: staging V pays from about 32 key tiles (its launch costs ~5 us)
+
+
+def attention(q, k, v, batch, lq, lk, heads, head_dim, ldq, ldkv, q_bs, kv_bs, out, ldo, o_bs, staged_v=None):
     """Multi-head attention over flat buffers; q/k/v/out may be views into wider projection buffers. bf16 inputs
-    with head_dim 64 stage V once per call as fp16 V^T tiles in the stream's cached workspace (the same output bits
-    as staged_v=False, which converts V in every query workgroup)."""
+    with head_dim 64 can stage V once per call as fp16 V^T tiles in the stream's cached workspace (the same output
+    bits as converting V in every query workgroup); staged_v=None stages from STAGED_V_MIN_KEYS keys on, True or
+    False forces the choice."""
     lib = load()
     dev = _require_cuda(q, k, v, out)
     if not (q.dtype == k.dtype == v.dtype):
         raise ValueError("q, k and v must share a dtype")
+    if staged_v is None:
+        staged_v = lk >= STAGED_V_MIN_KEYS
     need = int(lib.idolq_attention_workspace(_code(q), batch, lk, heads, head_dim)) if staged_v else 0
     ws = _attention_workspace(q.device, need) if need else None
     _check(lib.idolq_attention_ws(_ptr(q), _ptr(k), _ptr(v), _code(q), batch, lq, lk, heads, head_dim, ldq, ldkv,
