@@ -291,3 +291,32 @@ def test_attention_staged_v_tiles_give_the_same_bits(batch, lq, lk, heads):
     lib = L.load()
     assert lib.idolq_attention_workspace(L.BF16, batch, lk, heads, hd) >= batch * heads * ((lk + 63) // 64) * 8192
     assert lib.idolq_attention_workspace(L.F16, batch, lk, heads, hd) == 0
+
+
+def test_attention_workspace_entry_point_through_the_c_abi():
+    # idolq_attention_ws called directly: with its workspace (V staged), with one byte short of it (the call falls
+    # back to converting V in the workgroups) and through idolq_attention: the same bits each time
+    import ctypes
+    lib = L.load()
+    rng = np.random.default_rng(61)
+    batch, lq, lk, heads, hd = 2, 256, 640, 3, 64
+    dim = heads * hd
+    q, k, v = (to_dev(rng.normal(0, 1, (batch * n, dim)).astype(np.float32)).bfloat16() for n in (lq, lk, lk))
+    need = int(lib.idolq_attention_workspace(L.BF16, batch, lk, heads, hd))
+    assert need >= batch * heads * ((lk + 63) // 64) * 8192
+    ws = torch.empty(need, device=DEV, dtype=torch.uint8)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    outs = []
+    for nbytes in (need, need - 1, None):
+        out = torch.empty((batch * lq, dim), device=DEV, dtype=torch.bfloat16)
+        args = [ctypes.c_void_p(t.data_ptr()) for t in (q, k, v)] + [L.BF16, batch, lq, lk, heads, hd, dim, dim,
+                                                                    lq * dim, lk * dim, ctypes.c_void_p(out.data_ptr()),
+                                                                    L.BF16, dim, lq * dim]
+        if nbytes is None:
+            rc = lib.idolq_attention(*args, stream)
+        else:
+            rc = lib.idolq_attention_ws(*args, ctypes.c_void_p(ws.data_ptr()), nbytes, stream)
+        assert rc == 0, lib.idolq_last_error()
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
