@@ -417,3 +417,24 @@ def test_tiled_weights_match_row_major(m, n, k, off, cnt):
         assert torch.equal(raw, til)
     with pytest.raises(ValueError):
         L.gemm(x, wt, n, 16, 16, mode=L.MODE_DEQUANT, tiled=True)  # window not on a 32-row group
+
+
+def test_exact_on_tiled_weights_with_strided_activation_rows():
+    # x a column slice of a wider fp32 buffer (row stride 1280 > k = 1024): the split prepass reads the rows at their
+    # stride; the result matches the row-major EXACT kernel on the same view within 1e-6 and the oracle within 1e-5
+    rng = np.random.default_rng(71)
+    m, k, n = 150, 1024, 320
+    big = rng.normal(0, 1, (m, 1280)).astype(np.float32)
+    xb = to_dev(big)
+    x = xb[:, 64:64 + k]
+    wq = q8(rng, n, k)
+    wd = to_dev(wq)
+    wt = L.tile_q8_0(wd, n, k)
+    b = rng.normal(0, 0.01, n).astype(np.float32)
+    bt = to_dev(b)
+    raw = L.gemm(x, wd, n, bias=bt, mode=L.MODE_EXACT, out_dtype=torch.float32)
+    til = L.gemm(x, wt, n, bias=bt, mode=L.MODE_EXACT, out_dtype=torch.float32, tiled=True)
+    torch.cuda.synchronize()
+    assert norm_rel(til.cpu().numpy(), raw.cpu().numpy()) < 1e-6
+    ref = O.gemm_q8_float(np.ascontiguousarray(big[:, 64:64 + k]), wq, n, k, b)
+    assert norm_rel(til.cpu().numpy(), ref) < 1e-5
