@@ -438,3 +438,19 @@ def test_exact_on_tiled_weights_with_strided_activation_rows():
     assert norm_rel(til.cpu().numpy(), raw.cpu().numpy()) < 1e-6
     ref = O.gemm_q8_float(np.ascontiguousarray(big[:, 64:64 + k]), wq, n, k, b)
     assert norm_rel(til.cpu().numpy(), ref) < 1e-5
+
+
+def test_int8_on_tiled_weights_with_strided_activation_rows():
+    # bf16 x a column slice of a wider buffer (row stride 1600 > k = 1024): the tiled-layout quantizer reads the rows
+    # at their stride; whole tiles give the same bits as the row-major INT8 kernel on the same view
+    rng = np.random.default_rng(72)
+    m, k, n = 200, 1024, 256
+    xb = to_dev(rng.normal(0, 1, (m, 1600)).astype(np.float32)).bfloat16()
+    x = xb[:, 128:128 + k]
+    wd = to_dev(q8(rng, n, k))
+    wt = L.tile_q8_0(wd, n, k)
+    bt = to_dev(rng.normal(0, 0.01, n).astype(np.float32))
+    raw = L.gemm(x, wd, n, bias=bt, mode=L.MODE_INT8, out_dtype=torch.float32)
+    til = L.gemm(x, wt, n, bias=bt, mode=L.MODE_INT8, out_dtype=torch.float32, tiled=True)
+    torch.cuda.synchronize()
+    assert torch.equal(raw, til)
