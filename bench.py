@@ -491,12 +491,19 @@ def run_decoders(args):
 
 
 def run_fused_kinds(args):
-    """fused_linear (the packed-linear surface) for each fused kind at the MLP block's up-projection shape, bf16
-    x [4096, 1536] -> [4096, 6144] with bias: ms per call (20 calls after 3 warm-ups) and TFLOP/s."""
+    """The packed-linear surface for each fused kind at the MLP block's up-projection shape, bf16 x [4096, 1536] ->
+    [4096, 6144] with bias: PackedLinear layers with the fused path enabled (the reference pipeline's call,
+    tools/idol_packed.py:73-82), ms per call (20 calls after 3 warm-ups) and TFLOP/s; beside them fused_linear called
+    directly on the GGUF bytes (fused_q8_0_direct_ms) and the tiled-weight GEMM with the same bias and no activation
+    (fused_q8_0_tiled_gemm_ms), the kernel the layer's tiled copy runs."""
+    from types import SimpleNamespace
+
     import numpy as np
     import torch
     import idolq_lib as L
+    from ggml_types import GGMLQuantizationType as T
     from idol_hip import fused_linear
+    from idol_packed import PackedLinear, enable_fused_packed
 
     gen = torch.Generator(device="cuda").manual_seed(3)
     x = torch.randn(M, D, device="cuda", dtype=torch.bfloat16, generator=gen)
@@ -513,19 +520,33 @@ def run_fused_kinds(args):
     inv = torch.where(d != 0, 1.0 / d.float(), torch.zeros_like(d, dtype=torch.float32))
     q = torch.clamp(torch.trunc(g * inv + 8.5), max=15).to(torch.uint8)
     q4 = torch.cat([d.view(torch.uint8).reshape(-1, 2), q[:, :16] | (q[:, 16:] << 4)], dim=1).reshape(-1)
-    out = {}
-    for name, code, packed in (("q8_0", 8, q8), ("q4_0", 4, q4), ("q4_k", 44, torch.from_numpy(q4k).cuda().reshape(-1))):
+
+    def timed(fn):
         with torch.no_grad():
             for _ in range(3):
-                fused_linear(x, packed, (H, D), code, bias)
+                fn()
             torch.cuda.synchronize()
             t0 = time.perf_counter()
             for _ in range(20):
-                fused_linear(x, packed, (H, D), code, bias)
+                fn()
             torch.cuda.synchronize()
-        ms = (time.perf_counter() - t0) / 20 * 1e3
+        return (time.perf_counter() - t0) / 20 * 1e3
+
+    out = {}
+    for name, kind, packed in (("q8_0", T.Q8_0, q8), ("q4_0", T.Q4_0, q4), ("q4_k", T.Q4_K, torch.from_numpy(q4k))):
+        layer = PackedLinear(SimpleNamespace(shape=np.array([D, H]), tensor_type=kind,
+                                             data=packed.cpu().numpy().reshape(-1)), bias).to("cuda")
+        enable_fused_packed(layer)
+        ms = timed(lambda: layer(x))
         out[f"fused_{name}_ms"] = round(ms, 4)
         out[f"fused_{name}_tflops"] = round(2.0 * M * D * H / (ms * 1e-3) / 1e12, 1)
+    out["fused_q8_0_direct_ms"] = round(timed(lambda: fused_linear(x, q8, (H, D), 8, bias)), 4)
+    tiled, b32 = L.tile_q8_0(q8, H, D), bias.float()
+    y = torch.empty((M, H), device="cuda", dtype=torch.bfloat16)
+    out["fused_q8_0_tiled_gemm_ms"] = round(timed(lambda: L.gemm(x, tiled, H, bias=b32, mode=L.MODE_DEQUANT, out=y,
+                                                                  flags=L.FLAG_ROUND_BEFORE_BIAS, tiled=True)), 4)
+    out["fused_note"] = ("PackedLinear layers (fused path enabled) at bf16 [4096, 1536] -> 6144 with bias; Q8_0 and "
+                         "Q4_0 run their tiled Q8_0 copy, Q4_K its GGUF super-blocks")
     return out
 
 

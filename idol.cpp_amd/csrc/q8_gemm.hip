@@ -955,6 +955,10 @@ extern "C" int idolq_q8_0_gemm(const void* x, int x_dtype, int64_t m, int64_t k,
         if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || ((size_t)ldx * xsz) % 16 != 0 || (reinterpret_cast<uintptr_t>(w) & 15) != 0)
             return fail(IDOLQ_EINVAL, "the tiled EXACT GEMM needs 16-byte aligned activation rows and weights");
         if (p.groups <= 0) return fail(IDOLQ_EINVAL, "tiled weights: n_total exceeds the layout");
+        // the fold kernel addresses the high and low parts (row stride k, 2 bytes each) and the weight groups with
+        // 32-bit byte offsets
+        if (m * k * 2 >= (int64_t)UINT32_MAX || (int64_t)p.groups * (k / 64) * 2176 >= (int64_t)UINT32_MAX)
+            return fail(IDOLQ_EINVAL, "the tiled EXACT GEMM needs m * k * 2 and the weight layout below 2^32 bytes");
         uint16_t* hi = static_cast<uint16_t*>(workspace);
         uint16_t* lo = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + need / 2);
         char* rest = static_cast<char*>(workspace) + need;

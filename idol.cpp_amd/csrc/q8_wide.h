@@ -580,7 +580,8 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
     // sum of the block's products of fp32 activations and exact codes. The activations come as bf16 high and low
     // parts (x = hi + lo to within 2^-16 relative); per block and accumulator tile four v_mfma_f32_32x32x16_bf16
     // (the high parts' two 16-deep steps, then the low parts') sum into a fresh fp32 tile that is folded as
-    // fmaf(s, d, acc), block after block: the operations and order of the row-major EXACT kernel.
+    // fmaf(s, d, acc), block after block. The row-major EXACT kernel computes the same block sums and folds but
+    // adds even and odd blocks in two depth groups merged at the end, so the two paths agree to fp32 reassociation.
     auto codes_bf16 = [&](uint32_t lo, uint32_t hi) __attribute__((always_inline)) {
         uint32_t o[4];
 #pragma unroll

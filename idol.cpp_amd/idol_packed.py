@@ -20,6 +20,7 @@ _PACKED_KINDS = (GGMLQuantizationType.F16, GGMLQuantizationType.Q8_0, GGMLQuanti
 _BLOCK_KINDS = frozenset(_PACKED_KINDS[1:])
 _FUSED_KINDS = {GGMLQuantizationType.Q4_0: 4, GGMLQuantizationType.Q8_0: 8, GGMLQuantizationType.Q4_K: 44}
 _FUSED_DTYPES = (torch.float16, torch.bfloat16)
+_TILED_KINDS = (GGMLQuantizationType.Q8_0, GGMLQuantizationType.Q4_0)  # fused through the Q8_0 GEMM
 
 
 class PackedLinear(torch.nn.Module):
@@ -36,13 +37,34 @@ class PackedLinear(torch.nn.Module):
         self.shape, self.kind, self.fused = shape, source.tensor_type, False
         self.register_buffer("packed", torch.from_numpy(np.array(source.data, dtype=np.uint8, copy=True).reshape(-1)))
         self.bias = None if bias is None else torch.nn.Parameter(bias.detach(), requires_grad=False)
-        self._q8_blocks = None  # Q4_0: its exact Q8_0 re-encoding on the packed buffer's device, made once
+        # derived device copies, made once and remade when `packed` moves or is written (its storage or version
+        # changes): Q4_0's exact Q8_0 re-encoding, and the Q8_0 blocks in the tiled GEMM layout
+        self._q8_blocks = self._q8_tiled = None
+        self._q8_blocks_key = self._q8_tiled_key = None
+
+    def _packed_key(self):
+        return (self.packed.device, self.packed.data_ptr(), self.packed._version)
 
     def _q4_0_as_q8_0(self):
-        if self._q8_blocks is None or self._q8_blocks.device != self.packed.device:
+        if self._q8_blocks is None or self._q8_blocks_key != self._packed_key():
             n, k = self.shape
             self._q8_blocks = L.q4_0_to_q8_0(self.packed, n, k)
+            self._q8_blocks_key = self._packed_key()
         return self._q8_blocks
+
+    def _q8_0_tiled(self):
+        """The layer's Q8_0 blocks (Q4_0: their exact Q8_0 re-encoding) in the library's tiled layout on the packed
+        buffer's device, made on the first fused call there (k % 64 == 0; None otherwise). It costs
+        L.tiled_q8_0_bytes(n, k) bytes of device memory beside `packed` (about 1.06 bytes per weight) and serves the
+        calls of more than 16 rows with the tiled-weight GEMM (bit-identical products)."""
+        n, k = self.shape
+        if k % 64:
+            return None
+        if self._q8_tiled is None or self._q8_tiled_key != self._packed_key():
+            blocks = self._q4_0_as_q8_0() if self.kind == GGMLQuantizationType.Q4_0 else self.packed
+            self._q8_tiled = L.tile_q8_0(blocks, n, k)
+            self._q8_tiled_key = self._packed_key()
+        return self._q8_tiled
 
     def dequantize(self, dtype):
         """The dense (n, k) weight in `dtype` (tools/idol_packed.py:25-71)."""
@@ -71,7 +93,9 @@ class PackedLinear(torch.nn.Module):
     def forward(self, value):
         if self._fusable(value):
             q8 = self._q4_0_as_q8_0() if self.kind == GGMLQuantizationType.Q4_0 else None
-            return fused_linear(value, self.packed, self.shape, _FUSED_KINDS[self.kind], self.bias, q8_blocks=q8)
+            tiled = self._q8_0_tiled() if self.kind in _TILED_KINDS else None
+            return fused_linear(value, self.packed, self.shape, _FUSED_KINDS[self.kind], self.bias, q8_blocks=q8,
+                                q8_tiled=tiled)
         return F.linear(value, self.dequantize(value.dtype), self.bias)
 
 

@@ -124,6 +124,19 @@ def _row_stride(t):
     return max(t.stride(0), t.shape[1]) if t.shape[0] > 1 else t.shape[1]
 
 
+def _require_shape(t, rows, cols, name):
+    """A 2-D [rows, cols] tensor with unit-stride rows: the extent the library reads or writes through its pointer and
+    row stride, so a shorter or narrower view cannot send the kernel past the end of its memory."""
+    if t is None:
+        return
+    if t.dim() != 2 or tuple(t.shape) != (rows, cols):
+        raise ValueError(f"{name} must be a [{rows}, {cols}] tensor, got {list(t.shape)}")
+    if cols > 1 and t.stride(1) != 1:
+        raise ValueError(f"{name} needs a unit-stride last dimension")
+    if rows > 1 and t.stride(0) < cols:
+        raise ValueError(f"{name} rows overlap (row stride {t.stride(0)} < {cols})")
+
+
 def _require_cuda(*tensors):
     dev = None
     for t in tensors:
@@ -172,9 +185,13 @@ def gemm(x, w, n_total, n_offset=0, n=None, bias=None, residual=None, act=ACT_NO
     need a workspace (allocated here when none is given); on tiled weights split=True lets them use the rest of that
     workspace the same way."""
     lib = load()
+    if x.dim() != 2:
+        raise ValueError("x must be a 2-D [m, k] tensor")
     m, k = x.shape
     if n is None:
         n = n_total - n_offset
+    _require_shape(out, m, n, "out")
+    _require_shape(residual, m, n, "residual")
     dev = _require_cuda(x, w, bias, residual, out, workspace)
     if w.dtype != torch.uint8:
         raise ValueError("Q8_0 weights are a uint8 tensor")
@@ -216,9 +233,13 @@ def q4_k_gemm(x, w, n_total, n_offset=0, n=None, bias=None, residual=None, act=A
     (idolq_q4_k_gemm). x is bf16 or fp16 [m, k] with unit-stride rows; split=True passes the stream's DEQUANT
     workspace (stream-K)."""
     lib = load()
+    if x.dim() != 2:
+        raise ValueError("x must be a 2-D [m, k] tensor")
     m, k = x.shape
     if n is None:
         n = n_total - n_offset
+    _require_shape(out, m, n, "out")
+    _require_shape(residual, m, n, "residual")
     dev = _require_cuda(x, w, bias, residual, out)
     if w.dtype != torch.uint8 or w.numel() != int(lib.idolq_q4_k_bytes(n_total, k)) or not w.is_contiguous():
         raise ValueError("Q4_K weight size does not match its shape")
@@ -236,6 +257,11 @@ def q4_k_gemm(x, w, n_total, n_offset=0, n=None, bias=None, residual=None, act=A
                                _code(residual) if residual is not None else 0, ldr, act, flags, _ptr(out), _code(out),
                                _row_stride(out), _ptr(ws), ws.numel() if ws is not None else 0, _stream(dev)))
     return out
+
+
+def tiled_q8_0_bytes(n, k):
+    """Bytes of the tiled layout of an [n, k] Q8_0 matrix (rows padded to a multiple of 32; 0 unless k % 64 == 0)."""
+    return int(load().idolq_q8_0_tiled_bytes(n, k))
 
 
 def tile_q8_0(w, n, k):
@@ -320,11 +346,18 @@ def block_dots(qa, w, n_total, n_offset=0, n=None):
 
 def layernorm(x, eps, gamma=None, beta=None, shift=None, scale=None, rows_per_batch=0, out=None, out_dtype=None):
     lib = load()
-    _require_cuda(x, gamma, beta, shift, scale, out)
+    if x.dim() != 2:
+        raise ValueError("x must be a 2-D [rows, dim] tensor")
     rows, dim = x.shape
+    _require_shape(out, rows, dim, "out")
+    _require_cuda(x, gamma, beta, shift, scale, out)
     for v in (gamma, beta, shift, scale):
         if v is not None and (v.dtype != torch.float32 or not v.is_contiguous()):
             raise ValueError("gamma, beta, shift and scale are contiguous fp32 tensors")
+    batches = (rows + rows_per_batch - 1) // rows_per_batch if rows_per_batch > 0 and rows else 1
+    for v, need in ((gamma, dim), (beta, dim), (shift, batches * dim), (scale, batches * dim)):
+        if v is not None and v.numel() < need:
+            raise ValueError(f"gamma and beta need {dim} values, shift and scale {batches * dim}")
     if out is None:
         out = torch.empty((rows, dim), device=x.device, dtype=out_dtype or x.dtype)
     _check(lib.idolq_layernorm(_ptr(x), _code(x), rows, dim, _row_stride(x), eps, _ptr(gamma), _ptr(beta),

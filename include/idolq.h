@@ -51,8 +51,9 @@ enum { IDOLQ_MODE_AUTO = 0, IDOLQ_MODE_DEQUANT = 1, IDOLQ_MODE_EXACT = 2, IDOLQ_
 
 /* GEMM flags. ROUND_BEFORE_BIAS rounds the product to the output dtype before the bias is added, as the reference's
  * fused GPU path does (tools/idol_triton.py:84-89). TILED_WEIGHTS: w is in the tiled Q8_0 layout written by
- * idolq_q8_0_tile (DEQUANT mode with bf16/fp16 activations, or INT8 mode; activation rows 16-byte aligned,
- * k % 64 == 0, n_offset % 32 == 0). */
+ * idolq_q8_0_tile, in DEQUANT mode (bf16/fp16 activations), INT8 mode, or EXACT mode (fp32, bf16 or fp16 activations;
+ * it then needs a workspace of at least 2 * round_up(m * k * 2, 256) bytes for the activations' bf16 high and low
+ * parts); activation rows 16-byte aligned, weights 16-byte aligned, k % 64 == 0, n_offset % 32 == 0. */
 enum { IDOLQ_FLAG_ROUND_BEFORE_BIAS = 1, IDOLQ_FLAG_TILED_WEIGHTS = 2 };
 
 enum {
@@ -98,7 +99,11 @@ int idolq_q8_0_gemm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ld
 /* Workspace bytes idolq_q8_0_gemm uses for m rows of depth k in the given mode: the quantized activations and
  * scales, then room for the tiled path's split, for IDOLQ_MODE_INT8; the tile counters and partial tiles of the
  * current device's CUs for IDOLQ_MODE_DEQUANT; the high and low parts, then the same split room, for
- * IDOLQ_MODE_EXACT (used with tiled weights only: the row-major EXACT kernel takes no workspace). */
+ * IDOLQ_MODE_EXACT (used with tiled weights only: the row-major EXACT kernel takes no workspace).
+ * This is the most a call can use. The minimum a call requires is smaller, and a caller that sizes its buffer for
+ * row-major weights only may pass just that: INT8 round_up(m * k, 256) + round_up(m * (k / 32) * 4 + 16, 256) bytes
+ * (the split room, about 64 MiB on 256 CUs, serves tiled weights only); EXACT 0 on row-major weights and
+ * 2 * round_up(m * k * 2, 256) on tiled weights; DEQUANT 0 (without a workspace every tile is taken whole). */
 size_t idolq_q8_0_gemm_workspace(int64_t m, int64_t k, int mode);
 
 /* idolq_q8_0_gemm for callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses

@@ -333,6 +333,69 @@ def test_mlp_block_config_shape_parity_on_a_row_sample():
         assert torch.isfinite(y).all()
 
 
+def test_mlp_block_benchmarked_path_against_the_oracle():
+    # The MLP block exactly as bench.py times it: tiled weights with the split workspace (the up projection's launch
+    # plan at 4096 x 1536 -> 6144 is the split-column pair kernel, the down projection's 4096 x 6144 -> 1536 is
+    # stream-K), tanh-GELU and bias on the way up, bias and residual on the way down; then the down projection once
+    # more with the residual aliasing its output (y += h W^T + b, as the denoiser layers add into the stream).
+    # 64 sampled rows against the oracle's float kernel on the upcast inputs (2e-2, the DEQUANT bar), and against the
+    # oracle's dense fp32 kernel on the weights the DEQUANT arithmetic multiplies (each Q8_0 value rounded to bf16)
+    # within 1e-3 (the bar of the reference's fused test, tests/python/test_fused_packed.py:53-57), both rounded to
+    # bf16 as the GPU stores them; the down projection's 1e-3 check runs on the GPU's own h.
+    rng = np.random.default_rng(23)
+    M, D, H = 4096, 1536, 6144
+    x = to_dev(rng.normal(0, 1, (M, D)).astype(np.float32)).bfloat16()
+    wu, wd = q8(rng, H, D), q8(rng, D, H)
+    bu, bd = rng.normal(0, 0.01, H).astype(np.float32), rng.normal(0, 0.01, D).astype(np.float32)
+    tu, td = L.tile_q8_0(to_dev(wu), H, D), L.tile_q8_0(to_dev(wd), D, H)
+    h = torch.empty((M, H), device=DEV, dtype=torch.bfloat16)
+    y = torch.empty((M, D), device=DEV, dtype=torch.bfloat16)
+    L.gemm(x, tu, H, bias=to_dev(bu), act=L.ACT_GELU_TANH, mode=L.MODE_DEQUANT, out=h, tiled=True, split=True)
+    L.gemm(h, td, D, bias=to_dev(bd), residual=x, mode=L.MODE_DEQUANT, out=y, tiled=True, split=True)
+    acc = x.clone()
+    L.gemm(h, td, D, bias=to_dev(bd), residual=acc, mode=L.MODE_DEQUANT, out=acc, tiled=True, split=True)
+    torch.cuda.synchronize()
+    assert torch.equal(acc, y)  # aliasing the residual changes nothing
+    rows = rng.choice(M, 64, replace=False)
+    xs = x[rows].float().cpu().numpy()
+    wu_t, wd_t = rounded(O.q8_0_dequant(wu, H, D), torch.bfloat16), rounded(O.q8_0_dequant(wd, D, H), torch.bfloat16)
+    h_ref = rounded(O.gelu_tanh(O.gemm_q8_float(xs, wu, H, D, bu)), torch.bfloat16)
+    h_deq = rounded(O.gelu_tanh(O.gemm_dense(xs, wu_t, bu)), torch.bfloat16)
+    hs = h[rows].float().cpu().numpy()
+    assert norm_rel(hs, h_ref) < 2e-2 and norm_rel(hs, h_deq) < 1e-3
+    y_chain = rounded(O.gemm_q8_float(h_ref, wd, D, H, bd, residual=xs), torch.bfloat16)
+    y_deq = rounded(O.gemm_dense(hs, wd_t, bd) + xs, torch.bfloat16)
+    ys = y[rows].float().cpu().numpy()
+    assert norm_rel(ys, y_chain) < 2e-2 and norm_rel(ys, y_deq) < 1e-3
+    assert torch.isfinite(h).all() and torch.isfinite(y).all()
+    ws = L.split_workspace_of(x.device)
+    assert int(ws[:4096].view(torch.int32).abs().sum().item()) == 0  # every split tile was finished
+
+
+def test_wrappers_reject_wrong_dtypes_and_short_views_on_the_device():
+    # Outputs and residuals must cover [m, n] (a short-row view or a narrower column slice of a wider buffer is
+    # rejected before any launch) and have a dtype the library writes; a column slice of the right width inside a
+    # wider buffer is accepted and leaves the columns around it untouched.
+    rng = np.random.default_rng(24)
+    m, n, k = 64, 96, 128
+    x = to_dev(rng.normal(0, 1, (m, k)).astype(np.float32)).bfloat16()
+    w = to_dev(q8(rng, n, k))
+    wide = torch.zeros((m, n + 16), device=DEV, dtype=torch.bfloat16)
+    for bad in (wide[:m - 1, :n], wide[:, :n - 1], torch.zeros((m, n), device=DEV, dtype=torch.float64),
+                torch.zeros((m, n), device=DEV, dtype=torch.int32)):
+        with pytest.raises(ValueError):
+            L.gemm(x, w, n, out=bad, mode=L.MODE_DEQUANT)
+    with pytest.raises(ValueError):
+        L.gemm(x, w, n, residual=torch.zeros((m, n), device=DEV, dtype=torch.int16), mode=L.MODE_DEQUANT)
+    with pytest.raises(ValueError):
+        L.layernorm(x, 1e-6, out=torch.zeros((m, k), device=DEV, dtype=torch.int8))
+    with pytest.raises(ValueError):
+        L.layernorm(x, 1e-6, out=wide[:m // 2, :k])
+    L.gemm(x, w, n, out=wide[:, 8:8 + n], mode=L.MODE_DEQUANT)
+    ref = L.gemm(x, w, n, mode=L.MODE_DEQUANT)
+    assert torch.equal(wide[:, 8:8 + n], ref) and not wide[:, :8].any() and not wide[:, 8 + n:].any()
+
+
 def test_empty_and_tiny_inputs():
     rng = np.random.default_rng(18)
     w = q8(rng, 7, 64)

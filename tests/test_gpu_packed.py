@@ -108,3 +108,64 @@ def test_kernels_mirror_layer_norm_and_attention():
     K.attention(torch.from_numpy(q).to(DEV), lq, dim + 3, torch.from_numpy(kv).to(DEV), torch.from_numpy(kv).to(DEV),
                 lk, dim + 1, heads, hd, out, dim)
     assert norm_rel(out.cpu().numpy(), O.attention(q, kv, kv, lq, lk, dim + 3, dim + 1, heads, hd)) < 1e-5
+
+
+@pytest.mark.parametrize("kind", [T.Q8_0, T.Q4_0])
+def test_packed_linear_runs_its_tiled_copy_with_the_same_bits(kind):
+    # PackedLinear keeps the layer's Q8_0 blocks (Q4_0: their exact re-encoding) in the tiled GEMM layout, made once per
+    # device, and serves calls of more than 16 rows from it: layer(x) equals fused_linear on the GGUF bytes bit for
+    # bit (the tiled and row-major kernels compute the same products), shorter calls keep the row-major small-m
+    # kernel, and writing the packed bytes (load_state_dict) remakes the copy.
+    import idolq_lib as L
+    rng = np.random.default_rng(31)
+    n, k = 520, 1536
+    weights = rng.normal(0, 0.05, (n, k)).astype(np.float32)
+    data = O.q8_0_quantize(weights) if kind == T.Q8_0 else O.q4_0_quantize(weights)
+    layer = PackedLinear(SimpleNamespace(shape=np.array([k, n]), tensor_type=kind, data=data), None).to(DEV)
+    enable_fused_packed(layer)
+    code = 8 if kind == T.Q8_0 else 4
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    for dtype in (torch.bfloat16, torch.float16):
+        bias = torch.randn(n, device=DEV, dtype=dtype, generator=gen)
+        layer.bias = torch.nn.Parameter(bias, requires_grad=False)
+        for rows in (300, 7):
+            x = torch.randn(rows, k, device=DEV, dtype=dtype, generator=gen)
+            with torch.no_grad():
+                got = layer(x)
+                want = fused_linear(x, layer.packed, layer.shape, code, bias)
+            assert torch.equal(got, want), (dtype, rows)
+    assert layer._q8_tiled is not None and layer._q8_tiled.numel() == L.tiled_q8_0_bytes(n, k)
+    first = layer._q8_tiled
+    other = O.q8_0_quantize(weights[::-1].copy()) if kind == T.Q8_0 else O.q4_0_quantize(weights[::-1].copy())
+    layer.load_state_dict({"packed": torch.from_numpy(other), "bias": layer.bias.detach()})
+    x = torch.randn(64, k, device=DEV, dtype=torch.bfloat16, generator=gen)
+    layer.bias = None
+    with torch.no_grad():
+        assert torch.equal(layer(x), fused_linear(x, layer.packed, layer.shape, code))
+    assert layer._q8_tiled is not first
+
+
+def test_fp16_large_m_q8_0_adds_the_bias_before_its_rounding():
+    # tools/idol_triton.py:112-117: fp16 activations, m >= 4096, n >= 1024, k >= 1024 go through F.linear, whose fused
+    # bias enters the fp32 accumulator before the single rounding to fp16; below that size (and in bf16) the product
+    # is rounded first (tools/idol_triton.py:84-89). The output is compared element by element with both orders
+    # applied to an fp32 product of the dequantized weights: almost every element matches the branch's own order.
+    rng = np.random.default_rng(32)
+    n, k = 1024, 1024
+    w = O.q8_0_quantize(rng.normal(0, 0.25, (n, k)).astype(np.float32))
+    packed = torch.from_numpy(w).to(DEV)
+    dense = torch.from_numpy(O.q8_0_dequant(w, n, k)).to(DEV).half().float()
+    gen = torch.Generator(device=DEV).manual_seed(9)
+    bias = torch.randn(n, device=DEV, dtype=torch.float16, generator=gen)
+    for m, bias_first in ((4096, True), (4095, False)):
+        x = torch.randn(m, k, device=DEV, dtype=torch.float16, generator=gen)
+        with torch.no_grad():
+            y = fused_linear(x, packed, (n, k), 8, bias)
+        acc = x.float() @ dense.T
+        one = (acc + bias.float()).half()
+        two = (acc.half().float() + bias.float()).half()
+        match_one, match_two = (y == one).float().mean().item(), (y == two).float().mean().item()
+        if bias_first:
+            assert match_one > 0.99 and match_two < match_one - 0.05, (match_one, match_two)
+        else:
+            assert match_two > 0.99 and match_one < match_two - 0.05, (match_one, match_two)

@@ -86,9 +86,52 @@ def test_c_abi_rejects_bad_arguments_on_the_host():
     assert lib.idolq_activation(fake, L.F32, 10, 9, None) == L.EINVAL
     assert lib.idolq_pos_embed(fake, 4, fake, 16, fake, L.F32, 90, None) == L.EINVAL
     assert lib.idolq_copy2d(fake, L.F32, 4, fake, L.F32, 8, 2, 8, None) == L.EINVAL
+    # EXACT on tiled weights addresses its bf16 high / low parts and the weight groups with 32-bit byte offsets
+    big_ws = ctypes.c_size_t(1 << 36)
+    rc = lib.idolq_q8_0_gemm(fake, L.F32, 1 << 20, 2048, 2048, fake, 64, 0, 64, None, 0, None, 0, 0, 0, L.MODE_EXACT,
+                             L.FLAG_TILED_WEIGHTS, fake, L.F32, 64, fake, big_ws, None)
+    assert rc == L.EINVAL and b"2^32" in lib.idolq_last_error()
+    rc = lib.idolq_q8_0_gemm(fake, L.F32, 64, 64, 64, fake, 1 << 27, 0, 32, None, 0, None, 0, 0, 0, L.MODE_EXACT,
+                             L.FLAG_TILED_WEIGHTS, fake, L.F32, 32, fake, big_ws, None)
+    assert rc == L.EINVAL and b"2^32" in lib.idolq_last_error()
     # m == 0 or n == 0 is a no-op, as fused_linear's empty input is
     assert lib.idolq_q8_0_gemm(fake, L.BF16, 0, 64, 64, fake, 8, 0, 8, None, 0, None, 0, 0, 0, 0, 0, fake, L.BF16, 8,
                                None, 0, None) == 0
+
+
+def test_wrappers_reject_outputs_and_residuals_that_do_not_cover_the_result():
+    # The C ABI sees a pointer and a row stride only; the Python wrappers require every output and residual to be
+    # the [m, n] extent the kernel writes or reads, so a shorter or narrower view cannot send it past its memory.
+    # These checks come before any device work (CPU tensors reach them).
+    x = torch.zeros((64, 128), dtype=torch.bfloat16)
+    w = torch.zeros(L.q8_0_bytes(96, 128), dtype=torch.uint8)
+    big = torch.zeros((64, 200), dtype=torch.bfloat16)
+    for bad, what in ((torch.zeros((63, 96), dtype=torch.bfloat16), "out"),     # a row short
+                      (big[:32], "out"),                                         # a short-row view
+                      (big[:, :95], "out"),                                      # a column slice narrower than n
+                      (big[:, ::2][:, :96], "out"),                              # strided columns
+                      (torch.zeros(64 * 96, dtype=torch.bfloat16), "out")):      # not 2-D
+        with pytest.raises(ValueError, match=what):
+            L.gemm(x, w, 96, out=bad)
+    with pytest.raises(ValueError, match="residual"):
+        L.gemm(x, w, 96, residual=big[:60, :96])
+    with pytest.raises(ValueError, match="residual"):
+        L.gemm(x, w, 96, residual=big[:, :64])
+    with pytest.raises(ValueError, match="x must be"):
+        L.gemm(x.reshape(-1), w, 96)
+    # a window: out and the residual are [m, n] of the window, not of the whole layer
+    with pytest.raises(ValueError, match="out"):
+        L.gemm(x, w, 96, 32, 32, out=big[:, :96])
+    with pytest.raises(ValueError, match="out"):
+        L.q4_k_gemm(x, torch.zeros(1, dtype=torch.uint8), 96, out=big[:, :90])
+    with pytest.raises(ValueError, match="out"):
+        L.layernorm(x, 1e-6, out=big[:48, :128])
+    with pytest.raises(ValueError, match="out"):
+        L.layernorm(x, 1e-6, out=big[:, :100])
+    with pytest.raises(ValueError, match="rows overlap"):
+        L.layernorm(x, 1e-6, out=big.as_strided((64, 128), (100, 1)))
+    with pytest.raises(ValueError, match="x must be"):
+        L.layernorm(x[0], 1e-6)
 
 
 # ------------------------------------------------------------------------------------------------ fused_linear
