@@ -98,6 +98,14 @@ inline bool vec8_ok(const void* p, int dt, int64_t ld) {
     return reinterpret_cast<uintptr_t>(p) % 16 == 0 && (ld * (int64_t)dtype_size(dt)) % 16 == 0;
 }
 
+// v as an fp32 register value: the compiler may not fuse the operation that produced it with what consumes it (a
+// multiply followed by a 16-bit conversion would otherwise become one v_fma_mix with a single rounding, where the
+// fp32 result rounded to the output dtype is two).
+__device__ __forceinline__ float fp32_value(float v) {
+    asm("" : "+v"(v));
+    return v;
+}
+
 // Round a float through a dtype and back (identity for fp32).
 __device__ __forceinline__ float round_through(int dt, float v) {
     if (dt == IDOLQ_BF16) return bf16_bits_to_float(float_to_bf16_bits(v));

@@ -23,6 +23,32 @@ __device__ __forceinline__ double block_sum(double v, double* red) {
     return t;
 }
 
+// Sum of v over the wave's 64 lanes, in every lane: within each row of 16 lanes by four DPP steps (lanes i ^ 1,
+// i ^ 2 within quads, then the mirrored lanes of each half row and of the row: after each step every lane of a group
+// holds the group's sum, the same value, since the additions are commutative), then the four row sums read from
+// lanes 0, 16, 32, 48 and added as (r0 + r1) + (r2 + r3). A fixed order, so every kernel that reduces with it gets
+// the same bits; no LDS round trip (a shuffle of a double is two ds_bpermute).
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xf, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xf, 0xf, false);
+    return __builtin_bit_cast(double, ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+__device__ __forceinline__ double lane_f64(double v, int lane) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)u, lane);
+    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), lane);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ double wave_sum_f64(double v) {
+    v += dpp_f64<0xB1>(v);   // quad_perm(1, 0, 3, 2)
+    v += dpp_f64<0x4E>(v);   // quad_perm(2, 3, 0, 1)
+    v += dpp_f64<0x141>(v);  // row_half_mirror
+    v += dpp_f64<0x140>(v);  // row_mirror
+    return (lane_f64(v, 0) + lane_f64(v, 16)) + (lane_f64(v, 32) + lane_f64(v, 48));
+}
+
 // PER values per thread kept in registers (dim <= PER * 256); PER == 0 re-reads the row for each pass.
 template <int PER>
 __global__ __launch_bounds__(kThreads) void layernorm_kernel(const void* x, int x_dt, int64_t dim,
@@ -121,7 +147,7 @@ __global__ __launch_bounds__(256) void layernorm_rows_kernel(const T* x, int64_t
     for (int j = 0; j < NV; ++j)
 #pragma unroll
         for (int e = 0; e < E; ++e) sum += (double)v[j][e];
-    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    sum = wave_sum_f64(sum);
     const float mean = (float)(sum / (double)dim);
     double sq = 0.0;
 #pragma unroll
@@ -131,7 +157,7 @@ __global__ __launch_bounds__(256) void layernorm_rows_kernel(const T* x, int64_t
             const double t = (double)(v[j][e] - mean);
             sq = fma(t, t, sq);
         }
-    for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
+    sq = wave_sum_f64(sq);
     const float inv = 1.0f / sqrtf((float)(sq / (double)dim) + eps);
     const int64_t b = rows_per_batch > 0 ? r / rows_per_batch : 0;
     const float* sh = shift ? shift + b * dim : nullptr;
@@ -156,7 +182,7 @@ __global__ __launch_bounds__(256) void layernorm_rows_kernel(const T* x, int64_t
                 float t = (v[j][e + q] - mean) * inv;
                 if (gamma) t = fmaf(t, gg[q], beta ? bb[q] : 0.0f);
                 if (sc) t = fmaf(t, 1.0f + ss[q], hh[q]);
-                o[e + q] = t;
+                o[e + q] = fp32_value(t);
             }
         }
         uint32_t w[4];
@@ -172,10 +198,179 @@ __global__ __launch_bounds__(256) void layernorm_rows_kernel(const T* x, int64_t
     }
 }
 
+// Streaming rows (the HBM-bound form for many rows): each wave takes RPW consecutive rows, all in one adaLN batch,
+// and requests every 16-byte chunk of all of them, and its lanes' gamma / beta / shift / scale values, before it
+// computes anything; then it normalizes and stores the rows one after another, so the stores of the first rows go
+// out while the later rows' loads are still arriving, and the modulation vectors are read once per wave (not once
+// per row, after the reductions). Same per-row arithmetic as layernorm_rows_kernel: the same bits.
+template <typename T, int NV, int RPW, bool AFF, bool ADA>
+__global__ __launch_bounds__(256) void layernorm_stream_kernel(const T* x, int64_t rows, int64_t ldx, float eps,
+                                                                const float* __restrict__ gamma,
+                                                                const float* __restrict__ beta,
+                                                                const float* __restrict__ shift,
+                                                                const float* __restrict__ scale,
+                                                                int64_t rows_per_batch, T* y, int64_t ldy) {
+    // x may be y (in place): a wave requests all of its rows before it writes any of them
+    constexpr int E = 16 / sizeof(T);
+    constexpr int dim = 64 * NV * E;
+    const int lane = threadIdx.x & 63;
+    const int64_t r0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
+    if (r0 >= rows) return;
+    // the lane's columns (j * 64 + lane) * E .. + E - 1 of each parameter vector (the wave's rows share a batch),
+    // requested first: the row loads complete after them, so the first row's wait does not include them
+    const int64_t b = rows_per_batch > 0 ? r0 / rows_per_batch : 0;
+    const float* sh = shift ? shift + b * dim : nullptr;
+    const float* sc = scale ? scale + b * dim : nullptr;
+    float4 pg[NV][E / 4], pb[NV][E / 4], ps[NV][E / 4], ph[NV][E / 4];
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+        for (int q = 0; q < E / 4; ++q) {
+            const int c = (j * 64 + lane) * E + 4 * q;
+            if constexpr (AFF) {
+                pg[j][q] = *reinterpret_cast<const float4*>(gamma + c);
+                pb[j][q] = beta ? *reinterpret_cast<const float4*>(beta + c) : make_float4(0, 0, 0, 0);
+            }
+            if constexpr (ADA) {
+                ps[j][q] = *reinterpret_cast<const float4*>(sc + c);
+                ph[j][q] = *reinterpret_cast<const float4*>(sh + c);
+            }
+        }
+    // rows past the end read the last row (their results are not stored)
+    uint4 raw[RPW][NV];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+        const int64_t r = r0 + i < rows ? r0 + i : rows - 1;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) raw[i][j] = *reinterpret_cast<const uint4*>(x + r * ldx + (j * 64 + lane) * E);
+    }
+    float v[RPW][NV][E];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i)
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const uint32_t w[4] = {raw[i][j].x, raw[i][j].y, raw[i][j].z, raw[i][j].w};
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                if (sizeof(T) == 4) v[i][j][e] = __uint_as_float(w[e]);
+                else {
+                    const uint16_t bits = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+                    v[i][j][e] = std::is_same<T, __bf16>::value ? bf16_bits_to_float(bits) : half_bits_to_float(bits);
+                }
+            }
+        }
+    // each row is summed in the one-row-per-wave kernel's order; the RPW rows' sums and cross-lane steps are
+    // interleaved, so their latencies overlap
+    double sum[RPW], sq[RPW];
+    float mean[RPW], inv[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) sum[i] = 0.0;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+#pragma unroll
+            for (int i = 0; i < RPW; ++i) sum[i] += (double)v[i][j][e];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) sum[i] = wave_sum_f64(sum[i]);
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+        mean[i] = (float)(sum[i] / (double)dim);
+        sq[i] = 0.0;
+    }
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+#pragma unroll
+            for (int i = 0; i < RPW; ++i) {
+                const double t = (double)(v[i][j][e] - mean[i]);
+                sq[i] = fma(t, t, sq[i]);
+            }
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) sq[i] = wave_sum_f64(sq[i]);
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) inv[i] = 1.0f / sqrtf((float)(sq[i] / (double)dim) + eps);
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+        const int64_t r = r0 + i;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            float o[E];
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                const float4& g4 = pg[j][e / 4];
+                const float4& b4 = pb[j][e / 4];
+                const float4& s4 = ps[j][e / 4];
+                const float4& h4 = ph[j][e / 4];
+                const float gg = (&g4.x)[e % 4], bb = (&b4.x)[e % 4], ss = (&s4.x)[e % 4], hh = (&h4.x)[e % 4];
+                float t = (v[i][j][e] - mean[i]) * inv[i];
+                if constexpr (AFF) t = fmaf(t, gg, bb);
+                if constexpr (ADA) t = fmaf(t, 1.0f + ss, hh);
+                o[e] = fp32_value(t);
+            }
+            uint32_t w[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if (sizeof(T) == 4) w[q] = __float_as_uint(o[q]);
+                else if (std::is_same<T, __bf16>::value)
+                    w[q] = (uint32_t)float_to_bf16_bits(o[2 * q]) | ((uint32_t)float_to_bf16_bits(o[2 * q + 1]) << 16);
+                else
+                    w[q] = (uint32_t)float_to_half_bits(o[2 * q]) | ((uint32_t)float_to_half_bits(o[2 * q + 1]) << 16);
+            }
+            if (r < rows) *reinterpret_cast<uint4*>(y + r * ldy + (j * 64 + lane) * E) = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+    }
+}
+
+// Rows per wave of the streaming form, and the smallest row count it takes (below that, one row per wave spreads a
+// small call over more CUs).
+constexpr int kStreamRows = 4;
+constexpr int64_t kStreamMinRows = 4096;
+
+template <typename T>
+int launch_stream(const void* x, int64_t rows, int64_t dim, int64_t ldx, float eps, const float* gamma,
+                  const float* beta, const float* shift, const float* scale, int64_t rows_per_batch, void* y,
+                  int64_t ldy, hipStream_t s) {
+    constexpr int E = 16 / sizeof(T);
+    const int64_t per_wg = 4 * kStreamRows;
+    const dim3 grid((unsigned)((rows + per_wg - 1) / per_wg)), block(256);
+    const T* xt = static_cast<const T*>(x);
+    T* yt = static_cast<T*>(y);
+    auto go = [&](auto nv) {
+        constexpr int NV = decltype(nv)::value;
+        if (gamma && scale)
+            hipLaunchKernelGGL((layernorm_stream_kernel<T, NV, kStreamRows, true, true>), grid, block, 0, s, xt, rows,
+                               ldx, eps, gamma, beta, shift, scale, rows_per_batch, yt, ldy);
+        else if (gamma)
+            hipLaunchKernelGGL((layernorm_stream_kernel<T, NV, kStreamRows, true, false>), grid, block, 0, s, xt, rows,
+                               ldx, eps, gamma, beta, shift, scale, rows_per_batch, yt, ldy);
+        else if (scale)
+            hipLaunchKernelGGL((layernorm_stream_kernel<T, NV, kStreamRows, false, true>), grid, block, 0, s, xt, rows,
+                               ldx, eps, gamma, beta, shift, scale, rows_per_batch, yt, ldy);
+        else
+            hipLaunchKernelGGL((layernorm_stream_kernel<T, NV, kStreamRows, false, false>), grid, block, 0, s, xt, rows,
+                               ldx, eps, gamma, beta, shift, scale, rows_per_batch, yt, ldy);
+    };
+    switch (dim / (64 * E)) {
+        case 1: go(std::integral_constant<int, 1>{}); break;
+        case 2: go(std::integral_constant<int, 2>{}); break;
+        case 3: go(std::integral_constant<int, 3>{}); break;
+        case 4: go(std::integral_constant<int, 4>{}); break;
+        default: return -1;
+    }
+    return check_launch("layernorm_stream_kernel");
+}
+
 template <typename T>
 int launch_rows(const void* x, int64_t rows, int64_t dim, int64_t ldx, float eps, const float* gamma, const float* beta,
                 const float* shift, const float* scale, int64_t rows_per_batch, void* y, int64_t ldy, hipStream_t s) {
     constexpr int E = 16 / sizeof(T);
+    // many rows whose adaLN batches hold whole groups of kStreamRows rows: the streaming form
+    if (rows >= kStreamMinRows && (rows_per_batch <= 0 || rows_per_batch % kStreamRows == 0) && dim / (64 * E) <= 4) {
+        const int rc = launch_stream<T>(x, rows, dim, ldx, eps, gamma, beta, shift, scale, rows_per_batch, y, ldy, s);
+        if (rc != -1) return rc;
+    }
     const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
     const T* xt = static_cast<const T*>(x);
     T* yt = static_cast<T*>(y);
