@@ -76,9 +76,10 @@ GemmParams column_window(GemmParams p, int n0, int n) {
 
 // Launch plans, costed in microseconds from MI355X measurements: a 64-deep stage of a round of tiles takes STAGE, a
 // tile's fixed part (first loads; the epilogue, where the whole round's outputs are written at once, at the memory's
-// write rate) FIXED. Tiles: 256 x 256 (RT 8, CT 2) and 128 x 256 (4, 2). (128 x 384 tiles, which would make the MLP
-// block's and the denoiser's widths whole rounds, were measured 1.6x slower per stage: each dequantized weight
-// fragment then feeds 4 row tiles instead of 8, doubling the conversion work per MFMA.) Plans:
+// write rate) FIXED. Tiles: 256 x 256 (RT 8, CT 2), 128 x 256 (4, 2) and 128 x 384 (4, 3; whole tiles only, Q8_0 only).
+// 128 x 384 runs its main loop at about the 256 x 256 tile's time per MFMA (48 MFMAs per wave per stage against 64),
+// and makes n = 1536 at 8192 rows exactly one round (64 x 4 = 256 tiles, where 256 x 256 tiles leave 64 CUs idle);
+// split over k its finisher needs more registers than the 128 x 256 one, and it is not split. Plans:
 //   whole tiles of one shape;
 //   columns split in two ranges (one launch, q8_wide_pair_kernel): whole rounds of 256-row tiles on the first
 //     columns, 128-row tiles on the rest;
@@ -90,7 +91,7 @@ struct WideShape {
     int rt, ct;
     double stage, fixed;
 };
-constexpr WideShape kShapes[2] = {{8, 2, 1.42, 16.0}, {4, 2, 0.85, 9.0}};
+constexpr WideShape kShapes[3] = {{8, 2, 1.42, 16.0}, {4, 2, 0.85, 9.0}, {4, 3, 1.16, 12.0}};
 constexpr int kNumShapes = sizeof(kShapes) / sizeof(kShapes[0]);
 
 template <typename T, bool Q4K, int RT, int CT>
@@ -110,10 +111,11 @@ int launch_wide_dtype(GemmParams p, void* workspace, size_t workspace_bytes, hip
     bool best_split = false;
     for (int i = 0; i < kNumShapes; ++i) {
         const WideShape& c = kShapes[i];
+        if (Q4K && c.ct == 3) continue;
         const long tiles = tiles_of(c);
         const double whole = rounds(tiles) * (S * c.stage + c.fixed);
         if (best < 0 || whole < best) best = whole, best_shape = i, best_split = false;
-        if (c.rt == 4) {  // 256-row tiles are not split (below)
+        if (c.rt == 4 && c.ct == 2) {  // 256-row and 384-column tiles are not split (above)
             const long dp = tiles / cus * cus, units = (tiles - dp) * S;
             const size_t need = kCountBytes + (size_t)2 * cus * (32 * c.rt) * (128 * c.ct) * 4;
             if (workspace && workspace_bytes >= need && units >= cus) {
@@ -142,6 +144,9 @@ int launch_wide_dtype(GemmParams p, void* workspace, size_t workspace_bytes, hip
     WideSplit sp = whole(tiles);
     if (best_split) sp = split_plan(tiles, S, cus, workspace);
     if (best_shape == 0) return launch_wide_s<T, 8, 2, false, Q4K>(p, sp, stream);
+    if constexpr (!Q4K) {
+        if (best_shape == 2) return launch_wide_s<T, 4, 3, false, Q4K>(p, sp, stream);
+    }
     return launch_shape<T, Q4K, 4, 2>(p, sp, best_split, stream);
 }
 
