@@ -65,6 +65,11 @@ def parse():
                    help="launch only the MLP block's GEMMs in DEQUANT and INT8 mode and the config-2 self- and "
                         "cross-attention, 3 times each, untimed: the program the rocprofv3 --pmc counter passes "
                         "(MFMA busy cycles and ops, VALU instructions) run")
+    p.add_argument("--size-sweep", action="store_true",
+                   help="time idolq_layernorm (adaLN, bf16, dim 1536), the copy kernel (bf16, width 1536) and the "
+                        "small-m GEMV (m = 1, square Q8_0 weights) over a range of sizes, each on rotating buffers "
+                        "larger than the Infinity Cache, one JSON line per point: the per-launch fixed cost and the "
+                        "rate each kernel approaches")
     p.add_argument("--traffic-probe", action="store_true",
                    help="launch only the calibration copy (512 MiB bf16) and the two GEMMs, 3 times each, untimed: the "
                         "program rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs to measure HBM bytes per launch")
@@ -166,6 +171,64 @@ def run_counter_probe(args):
                     out, D, S * D)
     torch.cuda.synchronize()
     print(json.dumps({"counter_probe": "done"}), flush=True)
+
+
+def run_size_sweep(args):
+    """us per call and GB/s of layer norm, copy and GEMV at growing sizes (rotating buffers of >= 600 MB in total, so
+    every call reads HBM): where the rate stops growing with size, the remaining time is per-launch."""
+    import torch
+    import idolq_lib as L
+
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    shift = torch.randn((2, D), device="cuda", generator=gen) * 0.1
+    scale = torch.randn((2, D), device="cuda", generator=gen) * 0.1
+    for rows in (1024, 2048, 4096, 8192, 16384, 32768, 65536):
+        nb = max(2, int(600e6 // (rows * D * 4)))
+        xs = [torch.randn((rows, D), device="cuda", generator=gen).bfloat16() for _ in range(nb)]
+        ys = [torch.empty_like(x) for x in xs]
+        turn = [0]
+
+        def ln():
+            i = turn[0] % nb
+            turn[0] += 1
+            L.layernorm(xs[i], 1e-6, shift=shift, scale=scale, rows_per_batch=rows // 2, out=ys[i])
+
+        def cp():
+            i = turn[0] % nb
+            turn[0] += 1
+            L.copy2d(xs[i], ys[i])
+
+        for name, fn in (("layernorm_adaln_bf16", ln), ("copy_bf16", cp)):
+            for _ in range(nb):
+                fn()
+            us = gpu_time_us(torch, fn, max(20, 3 * nb))
+            nbytes = 2 * rows * D * 2
+            print(json.dumps({"sweep": name, "rows": rows, "dim": D, "bytes": nbytes, "us": round(us, 2),
+                              "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}), flush=True)
+        del xs, ys
+    for nk in (2048, 4096, 8192, 16384):
+        per = nk * nk // 32 * 34
+        nb = max(2, int(600e6 // per))
+        ws = [L.quantize_q8_0(torch.randn((nk, nk), device="cuda", generator=gen) * 0.02) for _ in range(nb)]
+        x = torch.randn((1, nk), device="cuda", generator=gen).bfloat16()
+        y = torch.empty((1, nk), device="cuda", dtype=torch.bfloat16)
+        turn = [0]
+
+        def gemv():
+            L.gemm(x, ws[turn[0] % nb], nk, mode=L.MODE_DEQUANT, out=y)
+            turn[0] += 1
+
+        for _ in range(nb):
+            gemv()
+        us = gpu_time_us(torch, gemv, max(20, 3 * nb))
+        nbytes = per + 4 * nk
+        print(json.dumps({"sweep": "gemv_q8_0_m1", "n": nk, "k": nk, "bytes": nbytes, "us": round(us, 2),
+                          "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}), flush=True)
+        del ws
+    a = torch.zeros((1, 8), device="cuda", dtype=torch.bfloat16)
+    b = torch.empty_like(a)
+    us = gpu_time_us(torch, lambda: L.copy2d(a, b), 200)
+    print(json.dumps({"sweep": "copy_16_bytes", "us": round(us, 2)}), flush=True)
 
 
 def measured_traffic():
@@ -755,6 +818,9 @@ def main():
         return
     if args.counter_probe:
         run_counter_probe(args)
+        return
+    if args.size_sweep:
+        run_size_sweep(args)
         return
     # The sections beside the headline run first: each is measured on its own, and the GPU has then been busy for a
     # while when the headline's warm-up steps start (its clocks ramp up over the first milliseconds of sustained
