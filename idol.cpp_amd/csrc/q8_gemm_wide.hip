@@ -159,8 +159,9 @@ bool wide_eligible(const GemmParams& p, int xt, int mode) {
            (int64_t)p.groups * (p.k / 64) * kGroupBytes < (int64_t)UINT32_MAX;
 }
 
-// tile counters, then two partial tiles of the split shape (128 x 256 fp32) per CU
-size_t wide_workspace_bytes() { return kCountBytes + (size_t)2 * cu_count() * 128 * 256 * 4; }
+// tile counters, then two partial tiles of the split shape (128 x 256 fp32) per workgroup slot: one per CU for
+// DEQUANT, two for the INT8 fold
+size_t wide_workspace_bytes() { return kCountBytes + (size_t)2 * kWideFoldSlots<kFoldI8> * cu_count() * 128 * 256 * 4; }
 
 namespace {
 template <bool Q4K>

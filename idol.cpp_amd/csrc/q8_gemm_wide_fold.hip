@@ -12,29 +12,33 @@ namespace {
 
 // 128 x 256 tiles (the fold's register budget), whole rounds or stream-K over the tiles left after them, costed like
 // the DEQUANT plans with the mode's stage time. The register epilogue takes bf16 outputs; others the general one.
+// INT8 runs two workgroups per CU (256 registers per lane and 78 KB of LDS each): its fold is bound by the vector ALU,
+// which one wave per SIMD leaves idle while it waits on its MFMA results and loads, and a second wave fills those
+// cycles. So a round is 2 x CUs tiles. EXACT (148 KB of LDS) runs one per CU.
 template <int FOLD>
 int launch_wide_fold(GemmParams p, double stage, void* workspace, size_t workspace_bytes, hipStream_t stream) {
     constexpr double kFixed = 9.0;
     set_y_vec4(p);
-    const long cus = cu_count(), S = p.k / 64;
+    const long slots = (long)kWideFoldSlots<FOLD> * cu_count(), S = p.k / 64;
     const long tiles = (long)((p.m + 127) / 128) * ((p.n + 255) / 256);
-    auto rounds = [&](long t) { return (t + cus - 1) / cus; };
-    const long dp = tiles / cus * cus, units = (tiles - dp) * S;
-    const size_t need = kCountBytes + (size_t)2 * cus * 128 * 256 * 4;
+    auto rounds = [&](long t) { return (t + slots - 1) / slots; };
+    const long dp = tiles / slots * slots, units = (tiles - dp) * S;
+    const size_t need = kCountBytes + (size_t)2 * slots * 128 * 256 * 4;
     const double whole = rounds(tiles) * (S * stage + kFixed);
-    const double split = (double)dp / cus * (S * stage + kFixed) + (double)rounds(units) * stage + 2 * kFixed + 6.0;
-    if (workspace && reinterpret_cast<uintptr_t>(workspace) % 256 == 0 && workspace_bytes >= need && units >= cus &&
+    const double split = (double)dp / slots * (S * stage + kFixed) + (double)rounds(units) * stage + 2 * kFixed + 6.0;
+    if (workspace && reinterpret_cast<uintptr_t>(workspace) % 256 == 0 && workspace_bytes >= need && units >= slots &&
         split < whole)
-        return launch_wide_s<__bf16, 4, 2, true, false, FOLD>(p, split_plan(tiles, S, cus, workspace), stream);
-    const WideSplit sp{(int)std::min(tiles, cus), 0, 0, 0, nullptr, nullptr, 1, 8};
+        return launch_wide_s<__bf16, 4, 2, true, false, FOLD>(p, split_plan(tiles, S, slots, workspace), stream);
+    const WideSplit sp{(int)std::min(tiles, slots), 0, 0, 0, nullptr, nullptr, 1, 8};
     return launch_wide_s<__bf16, 4, 2, false, false, FOLD>(p, sp, stream);
 }
 
 }  // namespace
 
-// p.qa / p.sa: the activation codes and scales in the tiled quantizer's layout (fold-bound: ~2 us per stage)
+// p.qa / p.sa: the activation codes and scales in the tiled quantizer's layout (fold-bound: a stage of a round of
+// two tiles per CU ~3 us)
 int launch_wide_i8(GemmParams p, void* workspace, size_t workspace_bytes, hipStream_t stream) {
-    return launch_wide_fold<kFoldI8>(p, 2.0, workspace, workspace_bytes, stream);
+    return launch_wide_fold<kFoldI8>(p, 3.0, workspace, workspace_bytes, stream);
 }
 
 // p.x / p.x_lo: the bf16 high and low parts of the activations, row stride k (MFMA-bound: twice DEQUANT's products)

@@ -87,6 +87,9 @@ struct WideSplit {
 // rows x 64 int8 codes, then the rows' two fp32 block scales), kFoldExact (the EXACT mode: BM rows x 64 bf16 high
 // parts, then BM rows x 64 bf16 low parts of fp32 activations).
 constexpr int kFoldI8 = 1, kFoldExact = 2;
+// workgroups per CU of each mode's kernel (its launch bounds; the INT8 fold runs two, see q8_gemm_wide_fold.hip)
+template <int FOLD>
+constexpr int kWideFoldSlots = FOLD == kFoldI8 ? 2 : 1;
 template <int RT, int CT, bool Q4K = false, int FOLD = 0>
 struct WideCfg {
     static constexpr bool I8 = FOLD == kFoldI8, EX = FOLD == kFoldExact;
@@ -878,7 +881,7 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
 }
 
 template <typename T, int RT, int CT, int ACT, bool FAST, bool RES, bool SPLIT, bool Q4K = false, int FOLD = 0>
-__global__ __launch_bounds__(kWideThreads) void q8_wide_kernel(GemmParams p, WideSplit sp) {
+__global__ __launch_bounds__(kWideThreads, kWideFoldSlots<FOLD>) void q8_wide_kernel(GemmParams p, WideSplit sp) {
     __shared__ __attribute__((aligned(1024))) char smem[WideCfg<RT, CT, Q4K, FOLD>::Lds];
     wide_tiles<T, RT, CT, ACT, FAST, RES, SPLIT, Q4K, FOLD>(p, sp, smem);
 }
