@@ -420,6 +420,36 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
+    // Without a residual (FAST), chunk q is staged finished: each accumulator rounded to T (when asked), plus its
+    // column's bias (bacc[c][g]: the 4 columns 32 c + 8 g + 4 (lane / 32) .. of the wave's range), through the
+    // activation -- the operations and order of the read-back path below, applied to a whole chunk's outputs at once
+    // so that their vector work (tanh-GELU: an exp2 and a reciprocal per output) is not interleaved with the output
+    // stores; the read-back then only converts to T.
+    auto stage_chunk_act = [&](float* st, auto qtag, const f32x4 (&bacc)[CT][4]) __attribute__((always_inline)) {
+        constexpr int q = decltype(qtag)::value;
+#pragma unroll
+        for (int h = 0; h < CH; ++h)
+#pragma unroll
+            for (int c = 0; c < CT; ++c)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const f32x16& a = acc[CH * q + h][c];
+                    f32x2 lo = {a[4 * g], a[4 * g + 1]}, hi = {a[4 * g + 2], a[4 * g + 3]};
+                    if (round_first) {
+                        lo = __builtin_convertvector(__builtin_convertvector(lo, T2), f32x2);
+                        hi = __builtin_convertvector(__builtin_convertvector(hi, T2), f32x2);
+                    }
+                    lo = lo + f32x2{bacc[c][g][0], bacc[c][g][1]};
+                    hi = hi + f32x2{bacc[c][g][2], bacc[c][g][3]};
+                    lo = f32x2{act_fast<ACT>(lo.x), act_fast<ACT>(lo.y)};
+                    hi = f32x2{act_fast<ACT>(hi.x), act_fast<ACT>(hi.y)};
+                    *reinterpret_cast<float4*>(st + (32 * h + (lane & 31)) * EP + 32 * c + 8 * g + 4 * (lane >> 5)) =
+                        make_float4(lo.x, lo.y, hi.x, hi.y);
+                }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
     auto chunk_done = [&]() __attribute__((always_inline)) {  // the next chunk reuses the staging rows just read
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -444,6 +474,17 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
         const __amdgpu_buffer_rsrc_t rb =
             __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.bias ? p.bias : p.y), 0, p.bias ? 0x7fffffff : 0, kRaw);
         const f32x4 b = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, col_ok ? (uint32_t)col * 4 : kOff, 0, 0));
+        f32x4 bacc[CT][4];  // !RES: the biases in the accumulator layout (stage_chunk_act)
+        if constexpr (!RES) {
+#pragma unroll
+            for (int c = 0; c < CT; ++c)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int ca = n0 + wave * 32 * CT + 32 * c + 8 * g + 4 * (lane >> 5);
+                    bacc[c][g] = __builtin_bit_cast(
+                        f32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, ca < p.n ? (uint32_t)ca * 4 : kOff, 0, 0));
+                }
+        }
         auto out_off = [&](int row, int64_t ld) __attribute__((always_inline)) {
             const bool ok = col_ok & (row < p.m);  // no short-circuit: a select, not a branch
             return ok ? (uint32_t)(row * (uint32_t)ld + col) * 2u : kOff;
@@ -468,26 +509,26 @@ __device__ __forceinline__ void wide_tiles(const GemmParams& p, const WideSplit&
         static_for<NQ>([&](auto qtag) __attribute__((always_inline)) {
             constexpr int q = decltype(qtag)::value;
             if (q >= 1 && q - 1 + PD < NQ) load_res(q - 1 + PD);
-            stage_chunk(st, qtag);
+            if constexpr (RES)
+                stage_chunk(st, qtag);
+            else
+                stage_chunk_act(st, qtag, bacc);
 #pragma unroll
             for (int i = 0; i < NR; ++i) {
                 const int lrow = RPI * i + rl, row = m0 + ER * q + lrow;
                 const float4 v4 = *reinterpret_cast<const float4*>(st + lrow * EP + 4 * cl);
                 f32x2 lo = {v4.x, v4.y}, hi = {v4.z, v4.w};
-                if (round_first) {
-                    lo = __builtin_convertvector(__builtin_convertvector(lo, T2), f32x2);
-                    hi = __builtin_convertvector(__builtin_convertvector(hi, T2), f32x2);
-                }
                 if constexpr (RES) {
+                    if (round_first) {
+                        lo = __builtin_convertvector(__builtin_convertvector(lo, T2), f32x2);
+                        hi = __builtin_convertvector(__builtin_convertvector(hi, T2), f32x2);
+                    }
                     const uint2 rr2 = r2[q % PD][i];
                     lo = lo + f32x2{b[0], b[1]} + __builtin_convertvector(__builtin_bit_cast(T2, rr2.x), f32x2);
                     hi = hi + f32x2{b[2], b[3]} + __builtin_convertvector(__builtin_bit_cast(T2, rr2.y), f32x2);
-                } else {
-                    lo = lo + f32x2{b[0], b[1]};
-                    hi = hi + f32x2{b[2], b[3]};
+                    lo = f32x2{act_fast<ACT>(lo.x), act_fast<ACT>(lo.y)};
+                    hi = f32x2{act_fast<ACT>(hi.x), act_fast<ACT>(hi.y)};
                 }
-                lo = f32x2{act_fast<ACT>(lo.x), act_fast<ACT>(lo.y)};
-                hi = f32x2{act_fast<ACT>(hi.x), act_fast<ACT>(hi.y)};
                 const i32x2 o = {__builtin_bit_cast(int, __builtin_convertvector(lo, T2)),
                                  __builtin_bit_cast(int, __builtin_convertvector(hi, T2))};
                 __builtin_amdgcn_raw_buffer_store_b64(o, ry, out_off(row, p.ldy), 0, 0);
