@@ -85,9 +85,13 @@ __global__ __launch_bounds__(256) void level_embed_kernel(float resolution, cons
 // the activation, each one fp32 operation, so every output is bit-identical to the reference's.
 // Workgroup: 256 threads own a 64 x 64 output tile, 4 x 4 outputs per thread (rows ty*4+i, columns tx*4+j); each
 // 32-deep chunk of x and W is staged in LDS depth-major, so the 4 operands a thread needs per step are one 16-byte
-// read each.
+// read each. VEC (y, and the bias and residual when given, 16-byte aligned with row strides a multiple of 4): a
+// thread's 4 columns of a row go out as one 16-byte store (the small-k products, such as the latent K/V projections
+// at k = 16, are bound by their output writes), the bias and residual come in as 16-byte loads; the arithmetic per
+// element is the same.
 constexpr int kGT = 64, kGK = 32, kGPitch = kGT + 4;
 
+template <bool VEC>
 __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__ x, int m, int k, int64_t ldx,
                                                        const float* __restrict__ w, int n,
                                                        const float* __restrict__ bias, const float* res, int64_t ldr,
@@ -131,6 +135,23 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
     for (int i = 0; i < 4; ++i) {
         const int row = m0 + ty * 4 + i;
         if (row >= m) continue;
+        if constexpr (VEC) {
+            const int col = n0 + tx * 4;
+            if (col + 3 < n) {
+                float4 v = make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+                if (bias) {
+                    const float4 b = *reinterpret_cast<const float4*>(bias + col);
+                    v.x += b.x, v.y += b.y, v.z += b.z, v.w += b.w;
+                }
+                if (res) {
+                    const float4 r = *reinterpret_cast<const float4*>(res + (int64_t)row * ldr + col);
+                    v.x += r.x, v.y += r.y, v.z += r.z, v.w += r.w;
+                }
+                v = make_float4(apply_act(act, v.x), apply_act(act, v.y), apply_act(act, v.z), apply_act(act, v.w));
+                *reinterpret_cast<float4*>(y + (int64_t)row * ldy + col) = v;
+                continue;
+            }
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int col = n0 + tx * 4 + j;
@@ -246,8 +267,14 @@ extern "C" int idolq_gemm_f32(const float* x, int64_t m, int64_t k, int64_t ldx,
     const int64_t gy = (m + kGT - 1) / kGT;
     if (gy > 65535) return fail(IDOLQ_EINVAL, "gemm_f32: more than 65535 * 64 rows");
     const dim3 grid((unsigned)((n + kGT - 1) / kGT), (unsigned)gy);
-    hipLaunchKernelGGL(gemm_f32_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), x, (int)m, (int)k, ldx,
-                       w, (int)n, bias, residual, ldr, act, y, ldy);
+    auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    const bool vec = a16(y) && ldy % 4 == 0 && (!bias || a16(bias)) && (!residual || (a16(residual) && ldr % 4 == 0));
+    if (vec)
+        hipLaunchKernelGGL(gemm_f32_kernel<true>, grid, dim3(256), 0, static_cast<hipStream_t>(stream), x, (int)m,
+                           (int)k, ldx, w, (int)n, bias, residual, ldr, act, y, ldy);
+    else
+        hipLaunchKernelGGL(gemm_f32_kernel<false>, grid, dim3(256), 0, static_cast<hipStream_t>(stream), x, (int)m,
+                           (int)k, ldx, w, (int)n, bias, residual, ldr, act, y, ldy);
     return check_launch("gemm_f32_kernel");
 }
 

@@ -499,6 +499,7 @@ def gemm_f32(x, w, bias=None, residual=None, act=ACT_NONE, out=None):
         raise ValueError("w must be a contiguous fp32 [n, k] matrix")
     if bias is not None and (bias.numel() != n or not bias.is_contiguous()):
         raise ValueError("bias must be n contiguous fp32 values")
+    _require_shape(out, m, n, "out")
     if out is None:
         out = torch.empty((m, n), device=x.device, dtype=torch.float32)
     if residual is not None and residual.shape != (m, n):

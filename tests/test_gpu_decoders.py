@@ -49,6 +49,34 @@ def test_gemm_f32_is_bit_identical_to_the_reference_dense_gemm(m, n, k):
     assert np.max(np.abs(got - ref64)) <= 1e-5 * max(1.0, np.max(np.abs(ref64)))
 
 
+def test_gemm_f32_output_paths_give_the_same_bits():
+    # 16-byte row stores (aligned output, the last columns of a row that does not fill 4 going out one by one) and
+    # the element-wise stores (an output view 4 bytes off alignment), each with a residual aliasing the output
+    _needs_ref()
+    rng = np.random.default_rng(5)
+    m, n, k = 50, 70, 16
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    w = (rng.standard_normal((n, k)) / 4).astype(np.float32)
+    b = rng.standard_normal(n).astype(np.float32)
+    res = rng.standard_normal((m, n)).astype(np.float32)
+    want = O.ref_gemm_dense(a, w, b)
+    want_res = O.ref_gemm_dense(a, w, b, residual=res)
+    assert np.array_equal(L.gemm_f32(_t(a), _t(w), bias=_t(b)).cpu().numpy(), want)
+    y = _t(res)
+    L.gemm_f32(_t(a), _t(w), bias=_t(b), residual=y, out=y)
+    assert np.array_equal(y.cpu().numpy(), want_res)
+    big = torch.zeros((m, n + 5), device=DEV, dtype=torch.float32)
+    view = big[:, 1:1 + n]  # data pointer 4 bytes past a 16-byte boundary, row stride n + 5
+    L.gemm_f32(_t(a), _t(w), bias=_t(b), out=view)
+    assert np.array_equal(view.cpu().numpy(), want)
+    view.copy_(_t(res))
+    L.gemm_f32(_t(a), _t(w), bias=_t(b), residual=view, out=view)
+    assert np.array_equal(view.cpu().numpy(), want_res)
+    assert not big[:, 0].any() and not big[:, 1 + n:].any()
+    with pytest.raises(ValueError):
+        L.gemm_f32(_t(a), _t(w), out=big[: m - 1, :n])  # an output with too few rows
+
+
 def test_gemm_f32_strided_rows_and_silu():
     rng = np.random.default_rng(1)
     a = rng.standard_normal((33, 80)).astype(np.float32)
