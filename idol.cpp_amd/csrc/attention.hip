@@ -573,64 +573,127 @@ __global__ __launch_bounds__(256) void attn_f32_mfma(AttnParams p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[t][r] = 0.0f;
 
-    // K and V of the next tile are loaded while the current one is multiplied (register double buffer)
-    float kn[HH], vn[DB][16];
-    auto load_tile = [&](int64_t k0) {
+    // Software-pipelined over the wave's tiles, three tiles in flight: in the step of tile t the matrix cores take the
+    // scores of tile t + 1 and the product of tile t - 1, alternating (two independent chains, so no MFMA waits on the
+    // one before it), while the vector ALU runs tile t's softmax between them (each of the 64 slots pinned by a
+    // scheduling barrier). K is loaded two tiles ahead and V one, into two register sets each; the probabilities wait
+    // one step for their product. Every value is computed as in a plain tile-by-tile loop, in the same order.
+    float ks[2][HH], vs[2][DB][16];
+    f32x16 ps[2], sc;  // probabilities of tiles awaiting their product; scores of the next tile
+    float alpha_p = 1.0f;  // tile t - 1's rescale factor, applied to o before its product
+    auto load_k = [&](int set, int64_t k0) __attribute__((always_inline)) {
         const float* kr = kbase + (k0 + col < lk ? k0 + col : lk - 1) * p.ldkv + half * HH;
 #pragma unroll
         for (int i = 0; i < HH; i += 4) {
             const f32x4 v = *reinterpret_cast<const f32x4*>(kr + i);
-            kn[i] = v[0], kn[i + 1] = v[1], kn[i + 2] = v[2], kn[i + 3] = v[3];
+            ks[set][i] = v[0], ks[set][i + 1] = v[1], ks[set][i + 2] = v[2], ks[set][i + 3] = v[3];
         }
+    };
+    auto load_v = [&](int set, int64_t k0) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
             const int64_t key = k0 + 8 * (j >> 2) + 4 * half + (j & 3);
             const float* vr = vbase + (key < lk ? key : lk - 1) * p.ldkv + col;
 #pragma unroll
-            for (int t2 = 0; t2 < DB; ++t2) vn[t2][j] = vr[t2 * 32];
+            for (int t2 = 0; t2 < DB; ++t2) vs[set][t2][j] = vr[t2 * 32];
         }
     };
-    if (t0 < t1) load_tile(t0 * 32);
-    for (int64_t t = t0; t < t1; ++t) {
+    // o *= alpha_p (skipped when every lane's factor is 1, which leaves o unchanged)
+    auto rescale = [&]() __attribute__((always_inline)) {
+        if (__builtin_amdgcn_ballot_w64(alpha_p != 1.0f) != 0) {
+#pragma unroll
+            for (int t2 = 0; t2 < DB; ++t2)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[t2][r] *= alpha_p;
+        }
+    };
+    // product MFMA q of the tile whose V is in vs[set] and probabilities in ps[set]: d block q % DB, key chunk q / DB
+    auto pv = [&](int set, int q) __attribute__((always_inline)) {
+        const int t2 = q % DB, j = q / DB;
+        o[t2] = __builtin_amdgcn_mfma_f32_32x32x2f32(vs[set][t2][j], ps[set][j], o[t2], 0, 0, 0);
+    };
+    // the step of tile t (parity P: its K was in ks[P], its V goes to vs[P], its probabilities to ps[P]); NEXT: tile
+    // t + 1 exists (its K in ks[P ^ 1]); PREV: tile t - 1 awaits its product (vs[P ^ 1], ps[P ^ 1])
+    auto step = [&](int64_t t, auto p_tag, auto next_tag, auto prev_tag) __attribute__((always_inline)) {
+        constexpr int P = decltype(p_tag)::value;
+        constexpr bool NEXT = decltype(next_tag)::value, PREV = decltype(prev_tag)::value;
         const int64_t k0 = t * 32;
-        float kv[HH], vv[DB][16];
+        load_v(P, k0);
+        if (NEXT && t + 2 < t1) load_k(P, k0 + 64);
+        if constexpr (PREV) rescale();
+        __builtin_amdgcn_sched_barrier(0);
+        f32x16 s = sc, acc;
 #pragma unroll
-        for (int i = 0; i < HH; ++i) kv[i] = kn[i];
+        for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+        float mx = -INFINITY, mxo = 0.0f, m_new = 0.0f, alpha = 0.0f, sum = 0.0f;
+        static_for<64>([&](auto I) __attribute__((always_inline)) {
+            constexpr int i = decltype(I)::value;
+            if constexpr (i % 2 == 0) {
+                if constexpr (NEXT && i / 2 < HH)
+                    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(ks[P ^ 1][i / 2], qv[i / 2], acc, 0, 0, 0);
+            } else {
+                if constexpr (PREV && i / 2 < 16 * DB) pv(P ^ 1, i / 2);
+            }
+            if constexpr (i < 16) {  // scale and mask score i, running maximum
+                const int64_t key = k0 + 8 * (i >> 2) + 4 * half + (i & 3);
+                s[i] = key < lk ? s[i] * c : -INFINITY;
+                mx = fmaxf(mx, s[i]);
+            } else if constexpr (i == 16) {
+                mxo = __shfl_xor(mx, 32);
+            } else if constexpr (i == 20) {
+                mx = fmaxf(mx, mxo);
+                m_new = fmaxf(m, mx);
+                alpha = exp2f(m - m_new);
+            } else if constexpr (i >= 21 && i < 37) {  // probability i - 21, summed in order
+                constexpr int r = i - 21;
+                s[r] = exp2f(s[r] - m_new);
+                sum += s[r];
+            } else if constexpr (i == 37) {
+                l = l * alpha + sum;
+                m = m_new;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        ps[P] = s;
+        alpha_p = alpha;
+        if constexpr (NEXT) sc = acc;
+    };
+    // the product of the last tile (parity P)
+    auto drain = [&](auto p_tag) __attribute__((always_inline)) {
+        constexpr int P = decltype(p_tag)::value;
+        rescale();
 #pragma unroll
-        for (int t2 = 0; t2 < DB; ++t2)
+        for (int q = 0; q < 16 * DB; ++q) pv(P, q);
+    };
+    const std::integral_constant<int, 0> p0;
+    const std::integral_constant<int, 1> p1;
+    const std::true_type yes;
+    const std::false_type no;
+    if (t0 < t1) {
+        load_k(0, t0 * 32);
+        if (t0 + 1 < t1) load_k(1, t0 * 32 + 32);
 #pragma unroll
-            for (int j = 0; j < 16; ++j) vv[t2][j] = vn[t2][j];
-        if (t + 1 < t1) load_tile(k0 + 32);
-        f32x16 s;
+        for (int r = 0; r < 16; ++r) sc[r] = 0.0f;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[r] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < HH; ++i) s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[i], qv[i], s, 0, 0, 0);
-
-        float mx = -INFINITY;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int64_t key = k0 + 8 * (r >> 2) + 4 * half + (r & 3);
-            s[r] = key < lk ? s[r] * c : -INFINITY;
-            mx = fmaxf(mx, s[r]);
+        for (int i = 0; i < HH; ++i) sc = __builtin_amdgcn_mfma_f32_32x32x2f32(ks[0][i], qv[i], sc, 0, 0, 0);
+        if (t0 + 1 < t1)
+            step(t0, p0, yes, no);
+        else
+            step(t0, p0, no, no);
+        int64_t t = t0 + 1;
+        for (; t + 2 < t1; t += 2) {
+            step(t, p1, yes, yes);
+            step(t + 1, p0, yes, yes);
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m, mx);
-        const float alpha = exp2f(m - m_new);
-        float sum = 0.0f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            s[r] = exp2f(s[r] - m_new);
-            sum += s[r];
-        }
-        l = l * alpha + sum;
-        m = m_new;
-#pragma unroll
-        for (int t2 = 0; t2 < DB; ++t2) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) o[t2][r] *= alpha;
-#pragma unroll
-            for (int j = 0; j < 16; ++j) o[t2] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[t2][j], s[j], o[t2], 0, 0, 0);
+        if (t + 1 < t1) {
+            step(t, p1, yes, yes);
+            step(t + 1, p0, no, yes);
+            drain(p0);
+        } else if (t < t1) {
+            step(t, p1, no, yes);
+            drain(p1);
+        } else {
+            drain(p0);
         }
     }
     l += __shfl_xor(l, 32);

@@ -7,6 +7,8 @@
 #include <cstddef>
 #include <cstdint>
 #include <string>
+#include <type_traits>
+#include <utility>
 
 #include "../../include/idolq.h"
 
@@ -19,6 +21,16 @@ typedef int i32x4 __attribute__((__vector_size__(4 * sizeof(int))));
 typedef float f32x4 __attribute__((__vector_size__(4 * sizeof(float))));
 typedef float f32x16 __attribute__((__vector_size__(16 * sizeof(float))));
 typedef int i32x16 __attribute__((__vector_size__(16 * sizeof(int))));
+
+// f(std::integral_constant<int, I>) for I = 0 .. N - 1, expanded at compile time (register-array indices stay constant)
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 constexpr int kQ8Block = 32;  // k values per Q8_0 block
 constexpr int kQ8Bytes = 34;  // fp16 scale + 32 int8 codes

@@ -109,16 +109,6 @@ struct WideCfg {
     static_assert(Lds <= 163840, "LDS budget");
 };
 
-// f(std::integral_constant<int, I>) for I = 0 .. N - 1, expanded at compile time (register-array indices stay constant)
-template <typename F, int... I>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
-    (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-    static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
 // (d * sc, dmin * m) of the 32-groups 2 pair and 2 pair + 1 of a Q4_K super-block from its 16-byte header (bytes 0-1
 // d, 2-3 dmin, 4-15 the 6-bit scales and minimums s[0..11]): for group j < 4, sc = s[j] & 63, m = s[4 + j] & 63; for
 // j >= 4, sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4), m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4). The products are
