@@ -263,6 +263,30 @@ def test_attention_raises_the_running_maximum(dtype):
         assert norm_rel(got[:, cols], torch.from_numpy(ref[:, cols]).to(dtype).float().numpy()) < 1e-3, h
 
 
+@pytest.mark.parametrize("hd", [32, 64])
+def test_attention_fp32_running_maximum_rises_tile_after_tile(hd):
+    # fp32 matrix-core kernel: scores that grow along the keys, so every tile raises the running maximum and rescales
+    # the output before its product, and one key far above all others; the waves walk 6, 6, 6 and 4 tiles of their
+    # quarters, so the pipelined loop's branches run with rescale factors below 1. Against the oracle and fp64.
+    rng = np.random.default_rng(28)
+    lq, lk, heads = 96, 700, 2
+    dim = heads * hd
+    q = rng.normal(0.5, 1, (lq, dim)).astype(np.float32)
+    k = (rng.normal(0.5, 1, (lk, dim)) * np.linspace(0.5, 4, lk)[:, None]).astype(np.float32)
+    k[450, :hd] = 6.0
+    v = rng.normal(0, 1, (lk, dim)).astype(np.float32)
+    out = torch.empty((lq, dim), device=DEV)
+    L.attention(to_dev(q), to_dev(k), to_dev(v), 1, lq, lk, heads, hd, dim, dim, 0, 0, out, dim, 0)
+    got = out.cpu().numpy()
+    assert norm_rel(got, O.attention(q, k, v, lq, lk, dim, dim, heads, hd)) < 1e-5
+    for h in range(heads):
+        cols = slice(h * hd, (h + 1) * hd)
+        s = q[:, cols].astype(np.float64) @ k[:, cols].astype(np.float64).T / np.sqrt(hd)
+        pr = np.exp(s - s.max(axis=1, keepdims=True))
+        o64 = (pr / pr.sum(axis=1, keepdims=True)) @ v[:, cols].astype(np.float64)
+        assert np.max(np.abs(got[:, cols] - o64)) < 2e-5, h
+
+
 def test_attention_bf16_values_beyond_fp16_range():
     # bf16 V holds values far beyond fp16's 65504 (the reference's fp32 attention takes them): the tiles that hold
     # them are staged with an exact power-of-two scale, so the output stays finite and within the 16-bit bar, with
