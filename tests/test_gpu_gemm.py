@@ -372,18 +372,20 @@ def test_mlp_block_benchmarked_path_against_the_oracle():
     assert int(ws[:4096].view(torch.int32).abs().sum().item()) == 0  # every split tile was finished
 
 
-@pytest.mark.parametrize("m,n,k", [(4096, 6144, 1536), (4096, 1536, 6144)])
-def test_benchmarked_launch_plans_scale_exactly_at_full_size(m, n, k):
-    # Every output of the benchmarked plans at full size (the split-column pair kernel for 4096 x 1536 -> 6144,
-    # stream-K for 4096 x 6144 -> 1536): scaling x by a power of two scales every product and every fp32 partial sum
-    # exactly, whatever tile, stage or stream-K part computed it, so the outputs must scale bit for bit. A misplaced
-    # row, column or partial tile anywhere breaks this.
+@pytest.mark.parametrize("mode", [L.MODE_DEQUANT, L.MODE_INT8])
+@pytest.mark.parametrize("m,n,k", [(4096, 6144, 1536), (4096, 1536, 6144), (8192, 1536, 1536)])
+def test_launch_plans_scale_exactly_at_full_size(m, n, k, mode):
+    # Every output of the full-size plans: the split-column pair kernel (DEQUANT, 4096 x 1536 -> 6144), stream-K
+    # (4096 x 6144 -> 1536), whole 128 x 384 tiles (8192 x 1536 -> 1536), and the INT8 fold with its two workgroups per
+    # CU. Scaling x by a power of two scales every product and every fp32 partial sum exactly, whatever tile, stage or
+    # stream-K part computed it; in INT8 mode it leaves the codes alone and scales the activation scales exactly. So
+    # the outputs must scale bit for bit, and a misplaced row, column or partial tile anywhere breaks this.
     rng = np.random.default_rng(m + n + k)
     x = to_dev(rng.normal(0, 1, (m, k)).astype(np.float32)).bfloat16()
     w = L.tile_q8_0(to_dev(q8(rng, n, k)), n, k)
-    y = L.gemm(x, w, n, mode=L.MODE_DEQUANT, tiled=True, split=True)
+    y = L.gemm(x, w, n, mode=mode, tiled=True, split=True)
     for f in (2.0, 0.25):
-        yf = L.gemm(x * f, w, n, mode=L.MODE_DEQUANT, tiled=True, split=True)
+        yf = L.gemm(x * f, w, n, mode=mode, tiled=True, split=True)
         assert torch.equal(yf, y * f), f
     assert torch.isfinite(y).all() and y.float().abs().max().item() > 0
 
