@@ -239,6 +239,29 @@ def test_self_attention_seq4096_sample():
     assert np.isfinite(got).all()
 
 
+@pytest.mark.parametrize("lk", [4096, 1024])
+def test_attention_full_size_scales_exactly_with_v(lk):
+    # Every output of the denoiser's attention shapes: self-attention over 4096 keys (V staged once as fp16 V^T
+    # tiles) and cross-attention over 1024 context keys (V converted in the workgroups), batch 2, 24 heads of 64.
+    # Scaling V up by a power of two scales each staged fp16 value, each P.V product and sum and the normalised output
+    # exactly, so the outputs must scale bit for bit; a misplaced key tile, head or query row anywhere breaks this.
+    # (Scaling down is not exact: V's smallest values become fp16 subnormals and lose bits.)
+    rng = np.random.default_rng(26 + lk)
+    B, S, heads, hd = 2, 4096, 24, 64
+    D = heads * hd
+    q = to_dev(rng.normal(0, 1, (B * S, D)).astype(np.float32)).bfloat16()
+    kv = to_dev(rng.normal(0, 1, (B * lk, 2 * D)).astype(np.float32)).bfloat16()
+    outs = []
+    for f in (1.0, 2.0, 4.0):
+        kvf = kv.clone()
+        kvf[:, D:] *= f
+        out = torch.empty((B * S, D), device=DEV, dtype=torch.bfloat16)
+        L.attention(q, kvf[:, :D], kvf[:, D:], B, S, lk, heads, hd, D, 2 * D, S * D, lk * 2 * D, out, D, S * D)
+        outs.append(out)
+    assert torch.isfinite(outs[0]).all()
+    assert torch.equal(outs[1], outs[0] * 2.0) and torch.equal(outs[2], outs[0] * 4.0)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_attention_raises_the_running_maximum(dtype):
     # scores that grow along the keys (key rows scaled from 0.5 to 4, positive means) and, in head 0, one key whose
