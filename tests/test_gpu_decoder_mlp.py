@@ -126,3 +126,14 @@ def test_point_mlp_full_size_runs_and_is_deterministic():
     b = model.forward(feats, coords)
     assert torch.isfinite(a).all() and torch.equal(a, b)
     assert model.flop(262144) == pytest.approx(90.66e9, rel=1e-3)
+
+
+def test_point_mlp_full_size_follows_a_permutation_of_the_points():
+    # Every point is computed on its own, whichever workgroup and row of its 32-point block it lands in, so permuting
+    # the 262144 points permutes the outputs bit for bit; a point read from or written to the wrong row breaks this.
+    model = PointMLP(seed=7)
+    feats, coords = inputs(262144, seed=8)
+    perm = torch.randperm(262144, generator=torch.Generator().manual_seed(9)).to(feats.device)
+    a = model.forward(feats, coords).clone()
+    b = model.forward(feats[perm].contiguous(), coords[perm].contiguous())
+    assert torch.equal(b, a[perm])
