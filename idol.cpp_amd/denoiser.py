@@ -71,6 +71,8 @@ class SyntheticDenoiser:
         self.q = torch.empty((rows, self.dim), device=device, dtype=bf16)
         self.kv = torch.empty((crow, 2 * self.dim), device=device, dtype=bf16)
         self.f = torch.empty((rows, mlp), device=device, dtype=bf16)
+        # every layer's context K/V projection in one GEMM per step (see batch_context_kv)
+        self.ckv_w = self.ckv_b = self.kv_all = None
 
     @classmethod
     def build(cls, layers=24, seed=0, batch=2, seq=4096, ctx_len=1024, heads=HEADS, head_dim=HEAD_DIM, mlp=MLP,
@@ -80,7 +82,22 @@ class SyntheticDenoiser:
         model.layers = [DenoiserLayer(gen, device, model.dim, mlp, ctx_dim) for _ in range(layers)]
         model.shift = torch.randn((batch, model.dim), device=device, generator=gen) * 0.1
         model.scale = torch.randn((batch, model.dim), device=device, generator=gen) * 0.1
+        model.batch_context_kv()
         return model
+
+    def batch_context_kv(self):
+        """Every layer reads the same context, so a step projects it for all layers in one GEMM: the layers' tiled
+        ckv weights side by side (the tiled layout is whole 32-row groups, so concatenated groups are the tiled
+        layout of the stacked matrix) and their biases, into one [batch * ctx_len, layers * 2 * dim] buffer whose
+        column slices the layers' cross-attentions read. One launch of len(layers) x 192 tiles fills the CUs where
+        each layer's 2048-row projection alone leaves a quarter of them idle; the sums are those of the per-layer
+        GEMMs (whole tiles, the same depth order)."""
+        if not self.layers or any("ckv" not in layer.wt for layer in self.layers):
+            return
+        self.ckv_w = torch.cat([layer.wt["ckv"] for layer in self.layers])
+        self.ckv_b = torch.cat([layer.b["ckv"] for layer in self.layers])
+        self.kv_all = torch.empty((self.batch * self.ctx_len, len(self.layers) * 2 * self.dim), device=self.device,
+                                  dtype=torch.bfloat16)
 
     def inputs(self, seed=1):
         gen = torch.Generator(device=self.device).manual_seed(seed)
@@ -89,8 +106,9 @@ class SyntheticDenoiser:
         return x, ctx
 
     # ---------------------------------------------------------------------------------------------------- blocks
-    def attention_block(self, layer, x, ctx, ada=True):
-        """Pre-LN self attention and cross attention with residuals, updating x in place."""
+    def attention_block(self, layer, x, ctx, ada=True, kv=None):
+        """Pre-LN self attention and cross attention with residuals, updating x in place. kv: the layer's context
+        K and V ([batch * ctx_len, 2 * dim], any row stride) when already projected; otherwise projected here."""
         B, S, Lc, D3 = self.batch, self.seq, self.ctx_len, 3 * self.dim
         D = self.dim
         if ada:
@@ -103,9 +121,12 @@ class SyntheticDenoiser:
         layer.linear("out", self.attn, x, residual=x)
         L.layernorm(x, 1e-6, out=self.h)
         layer.linear("cq", self.h, self.q)
-        layer.linear("ckv", ctx, self.kv)
-        L.attention(self.q, self.kv[:, :D], self.kv[:, D:], B, S, Lc, self.heads, self.head_dim, D, 2 * D,
-                    S * D, Lc * 2 * D, self.attn, D, S * D)
+        if kv is None:
+            layer.linear("ckv", ctx, self.kv)
+            kv = self.kv
+        ldkv = kv.stride(0)
+        L.attention(self.q, kv[:, :D], kv[:, D:], B, S, Lc, self.heads, self.head_dim, D, ldkv,
+                    S * D, Lc * ldkv, self.attn, D, S * D)
         layer.linear("cout", self.attn, x, residual=x)
         return x
 
@@ -117,8 +138,12 @@ class SyntheticDenoiser:
 
     def step(self, x, ctx):
         """One denoising step over all layers; x (bf16 [batch * seq, dim]) is updated in place and returned."""
-        for layer in self.layers:
-            self.attention_block(layer, x, ctx)
+        D2 = 2 * self.dim
+        if self.kv_all is not None:
+            L.gemm(ctx, self.ckv_w, self.kv_all.shape[1], bias=self.ckv_b, out=self.kv_all, tiled=True, split=True)
+        for i, layer in enumerate(self.layers):
+            kv = self.kv_all[:, i * D2:(i + 1) * D2] if self.kv_all is not None else None
+            self.attention_block(layer, x, ctx, kv=kv)
             self.mlp_block(layer, x)
         return x
 

@@ -108,3 +108,20 @@ def test_denoiser_step_full_size_runs_and_is_deterministic():
     model.step(x2, ctx)
     assert torch.isfinite(x).all() and torch.equal(x, x2)
     assert model.flop_per_step() == pytest.approx(814.97e9, rel=1e-4)
+
+
+def test_denoiser_step_with_batched_context_projection_equals_the_layer_by_layer_path():
+    # step() projects the context for every layer in one GEMM (the layers' tiled ckv weights side by side) and hands
+    # each cross-attention a column slice of the result; taking the layers one by one, each projecting its own
+    # context, must give the same bits (whole tiles, the same depth order per output)
+    B, S, Lc, heads, hd, mlp, cdim = 2, 160, 96, 2, 64, 512, 256
+    model = SyntheticDenoiser.build(layers=3, seed=11, batch=B, seq=S, ctx_len=Lc, heads=heads, head_dim=hd, mlp=mlp,
+                                    ctx_dim=cdim)
+    assert model.kv_all is not None and model.kv_all.shape == (B * Lc, 3 * 2 * heads * hd)
+    x, ctx = model.inputs(seed=12)
+    x2 = x.clone()
+    model.step(x, ctx)
+    for layer in model.layers:
+        model.attention_block(layer, x2, ctx)
+        model.mlp_block(layer, x2)
+    assert torch.isfinite(x).all() and torch.equal(x, x2)
