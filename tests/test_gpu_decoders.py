@@ -30,7 +30,8 @@ def _needs_ref():
 
 
 # ------------------------------------------------------------------------------------------------ operators
-@pytest.mark.parametrize("m,n,k", [(1, 64, 256), (37, 64, 3), (29, 128, 16), (70, 48, 100), (130, 200, 64), (5, 8, 1024)])
+@pytest.mark.parametrize("m,n,k", [(1, 64, 256), (37, 64, 3), (29, 128, 16), (70, 48, 100), (130, 200, 64), (5, 8, 1024),
+                                   (77, 520, 32), (300, 1024, 16)])
 def test_gemm_f32_is_bit_identical_to_the_reference_dense_gemm(m, n, k):
     _needs_ref()
     rng = np.random.default_rng(m * 7 + n)
@@ -75,6 +76,31 @@ def test_gemm_f32_output_paths_give_the_same_bits():
     assert not big[:, 0].any() and not big[:, 1 + n:].any()
     with pytest.raises(ValueError):
         L.gemm_f32(_t(a), _t(w), out=big[: m - 1, :n])  # an output with too few rows
+
+
+@pytest.mark.parametrize("k", [1, 16, 32])
+@pytest.mark.parametrize("act", [L.ACT_NONE, L.ACT_GELU_TANH])
+def test_gemm_f32_vector_and_element_paths_agree_at_small_depth(k, act):
+    # the 16-byte row stores (aligned output, n % 4 == 0) and the element-wise stores (an output view 4 bytes off
+    # alignment) give the same bits at the latent projections' small depths, with an activation, with and without a
+    # residual aliasing the output, over a partial last column tile and a partial last row tile
+    rng = np.random.default_rng(k + 10 * act)
+    m, n = 77, 520
+    a = _t(rng.standard_normal((m, k)).astype(np.float32))
+    w = _t((rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32))
+    b = _t(rng.standard_normal(n).astype(np.float32))
+    res = _t(rng.standard_normal((m, n)).astype(np.float32))
+    fast = L.gemm_f32(a, w, bias=b, act=act)
+    big = torch.zeros((m, n + 5), device=DEV, dtype=torch.float32)
+    view = big[:, 1:1 + n]
+    L.gemm_f32(a, w, bias=b, act=act, out=view)
+    assert torch.equal(fast, view)
+    y = res.clone()
+    L.gemm_f32(a, w, bias=b, residual=y, act=act, out=y)
+    view.copy_(res)
+    L.gemm_f32(a, w, bias=b, residual=view, act=act, out=view)
+    assert torch.equal(y, view)
+    assert not big[:, 0].any() and not big[:, 1 + n:].any()
 
 
 def test_gemm_f32_strided_rows_and_silu():
